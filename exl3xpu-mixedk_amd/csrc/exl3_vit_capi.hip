@@ -1,0 +1,467 @@
+// exl3_vit_capi.hip -- C-ABI of libexl3vit.so (declared in include/exl3_vit.h).
+//
+// Host-side orchestration of the gfx950 trellis kernels: argument checks with
+// the reference's status codes (quantize/viterbi_esimd.cpp:924-1005), the
+// codebook tables, per-device grow-only scratch, chunking of large batches and
+// the two-pass tail-biting schedule
+//     forward(pass 1) -> traceback(pass 1: ov) -> forward(pass 2) -> traceback
+// (quantize.py:323-354).
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <mutex>
+#include <vector>
+
+#include "../../include/exl3_vit.h"
+#include "viterbi_kernels.h"
+
+namespace {
+
+enum Code { kMul1 = 0, k3Inst = 1, kMcg = 2, kNumCodes = 3 };
+
+// --------------------------------------------------------- codebook tables
+// fp16 bits -> double (exact).
+double half_to_double(uint16_t h) {
+    const int sgn = (h >> 15) & 1, e = (h >> 10) & 31, m = h & 1023;
+    double v;
+    if (e == 0) v = ldexp((double)m, -24);
+    else if (e == 31) v = m ? NAN : INFINITY;
+    else v = ldexp((double)(1024 + m), e - 25);
+    return sgn ? -v : v;
+}
+
+// double -> fp16 bits, round to nearest, ties to even (finite inputs).
+uint16_t double_to_half(double v) {
+    uint16_t sgn = (v < 0 || (v == 0 && signbit(v))) ? 0x8000 : 0;
+    double a = fabs(v);
+    if (a == 0) return sgn;
+    int e;
+    frexp(a, &e);            // a = m * 2^e, m in [0.5, 1)
+    int ue = e - 1;          // a in [2^ue, 2^(ue+1))
+    if (ue < -14) {          // subnormal: quantum 2^-24
+        double q = nearbyint(ldexp(a, 24));
+        return sgn | (uint16_t)q;   // q == 1024 encodes the smallest normal
+    }
+    double q = nearbyint(ldexp(a, 10 - ue));  // in [1024, 2048]
+    if (q >= 2048) { q = 1024; ++ue; }
+    if (ue + 15 >= 31) return sgn | 0x7C00;
+    return sgn | (uint16_t)(((ue + 15) << 10) | ((int)q - 1024));
+}
+
+// Codebook tables, restating quantize.py:56-81 (_local_code_lut).
+void make_lut16(Code code, uint16_t* out) {
+    for (uint32_t s = 0; s < 65536u; ++s) {
+        if (code == kMul1) {
+            const uint32_t x = s * 0x83DCD12Du;
+            const uint32_t bs = (x & 0xFF) + ((x >> 8) & 0xFF) + ((x >> 16) & 0xFF) + (x >> 24);
+            const double h = 1024.0 + bs;
+            out[s] = double_to_half(h * half_to_double(0x1EEE) + half_to_double(0xC931));
+        } else {
+            uint32_t x = (code == k3Inst) ? s * 89226354u + 64248484u : s * 0xCBAC1FEDu;
+            x = (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
+            const double lo = half_to_double((uint16_t)(x & 0xFFFF));
+            const double hi = half_to_double((uint16_t)(x >> 16));
+            out[s] = double_to_half(lo + hi);
+        }
+    }
+}
+
+int parse_code(const char* code, Code* out) {
+    if (!code) return 12;
+    if (!strcmp(code, "mul1") || !strcmp(code, "exl3_mul1")) { *out = kMul1; return 0; }
+    if (!strcmp(code, "3inst") || !strcmp(code, "exl3_3inst")) { *out = k3Inst; return 0; }
+    if (!strcmp(code, "mcg") || !strcmp(code, "exl3_mcg")) { *out = kMcg; return 0; }
+    return 8;
+}
+
+// ------------------------------------------------------------ device state
+struct DevCtx {
+    bool ready = false;
+    int ncu = 0;
+    uint16_t* lut16[kNumCodes] = {nullptr, nullptr, nullptr};
+    uint32_t* err = nullptr;
+    void* bp = nullptr;
+    size_t bp_cap = 0;
+    int32_t* send = nullptr;
+    int32_t* ov = nullptr;
+    size_t seq_cap = 0;
+    float* hx = nullptr;       // staging for the host-pointer entries
+    int32_t* hs = nullptr;
+    size_t host_cap = 0;
+    size_t owned = 0;          // device bytes held
+};
+
+std::mutex g_mu;
+std::vector<DevCtx> g_dev;
+bool g_env_read = false;
+long long g_maxseq = 1LL << 24;
+size_t g_maxbytes = (size_t)64 << 30;
+size_t g_scratch = (size_t)8 << 30;
+
+void read_env() {
+    if (g_env_read) return;
+    if (const char* e = getenv("XTQ_VIT_MAXSEQ")) g_maxseq = atoll(e);
+    if (const char* e = getenv("XTQ_VIT_MAXBYTES")) g_maxbytes = strtoull(e, nullptr, 10);
+    if (const char* e = getenv("XTQ_VIT_SCRATCH")) g_scratch = strtoull(e, nullptr, 10);
+    g_env_read = true;
+}
+
+// Makes `dev` ready on the calling thread (which must have it current).
+int dev_init(int dev) {
+    read_env();
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0) {
+        fprintf(stderr, "xtq_vit: no HIP device\n");
+        return 1;
+    }
+    if ((int)g_dev.size() < ndev) g_dev.resize(ndev);
+    DevCtx& cx = g_dev[dev];
+    if (cx.ready) return 0;
+    if (hipDeviceGetAttribute(&cx.ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 1;
+    std::vector<uint16_t> h(65536);
+    for (int c = 0; c < kNumCodes; ++c) {
+        if (hipMalloc((void**)&cx.lut16[c], 65536 * sizeof(uint16_t)) != hipSuccess) return 2;
+        make_lut16((Code)c, h.data());
+        if (hipMemcpy(cx.lut16[c], h.data(), 65536 * sizeof(uint16_t), hipMemcpyHostToDevice) !=
+            hipSuccess)
+            return 1;
+    }
+    if (hipMalloc((void**)&cx.err, sizeof(uint32_t)) != hipSuccess) return 2;
+    if (hipMemset(cx.err, 0, sizeof(uint32_t)) != hipSuccess) return 1;
+    cx.owned = kNumCodes * 65536 * sizeof(uint16_t) + 256;
+    cx.ready = true;
+    return 0;
+}
+
+int current_device(int* dev) {
+    return hipGetDevice(dev) == hipSuccess ? 0 : 1;
+}
+
+// Device selected by XTQ_VIT_DEVIDX (host-pointer entries), else current.
+int host_entry_device(int* dev) {
+    if (const char* e = getenv("XTQ_VIT_DEVIDX")) {
+        int ndev = 0;
+        if (hipGetDeviceCount(&ndev) != hipSuccess) return 1;
+        const int idx = atoi(e);
+        if (idx < 0 || idx >= ndev) {
+            fprintf(stderr, "xtq_vit: XTQ_VIT_DEVIDX=%d, %d gpus\n", idx, ndev);
+            return 3;
+        }
+        *dev = idx;
+        return 0;
+    }
+    return current_device(dev);
+}
+
+template <typename P>
+int grow(P** p, size_t* cap, size_t want, size_t elem, size_t* owned) {
+    if (want <= *cap) return 0;
+    if (*p) {
+        (void)hipFree(*p);
+        *owned -= *cap * elem;
+    }
+    *p = nullptr;
+    *cap = 0;
+    if (hipMalloc((void**)p, want * elem) != hipSuccess) {
+        *p = nullptr;
+        return 2;
+    }
+    *cap = want;
+    *owned += want * elem;
+    return 0;
+}
+
+int check_common(int nseq, int K, int margin, int pivot) {
+    if (nseq <= 0 || nseq > g_maxseq) {
+        fprintf(stderr, "xtq_vit: nseq %d out of range (XTQ_VIT_MAXSEQ %lld)\n", nseq, g_maxseq);
+        return 6;
+    }
+    if (K < 2 || K > 7) return 9;
+    if (pivot < 0 || pivot >= xtq::kSteps || margin < 0) return 10;
+    return 0;
+}
+
+// Sequences per chunk for a scratch budget.
+int chunk_size(const DevCtx& cx, int K, int nseq) {
+    const size_t per = xtq::bp_tile_bytes(K);
+    size_t ch = g_scratch / per;
+    if (ch < 1) ch = 1;
+    const size_t round = (size_t)4 * (cx.ncu > 0 ? cx.ncu : 1);
+    if (ch > round) ch -= ch % round;
+    if (ch > (size_t)nseq) ch = nseq;
+    return (int)ch;
+}
+
+// The two-pass tail-biting schedule over device buffers (quantize.py:323-354).
+int run_tailbite(DevCtx& cx, const float* dX, int nseq, int K, Code code, int margin,
+                 int pivot, int32_t* d_states, int16_t* d_trellis, hipStream_t s) {
+    const int chunk = chunk_size(cx, K, nseq);
+    const size_t per = xtq::bp_tile_bytes(K);
+    // Device bytes this call adds to what the library already holds.
+    size_t add = 0;
+    if ((size_t)chunk * per > cx.bp_cap) add += (size_t)chunk * per - cx.bp_cap;
+    if ((size_t)chunk > cx.seq_cap) add += ((size_t)chunk - cx.seq_cap) * 2 * sizeof(int32_t);
+    if (cx.owned + add > g_maxbytes) {
+        fprintf(stderr, "xtq_vit: request over XTQ_VIT_MAXBYTES (%zu)\n", g_maxbytes);
+        return 5;
+    }
+    size_t bpcap_bytes = cx.bp_cap;
+    if (grow((uint8_t**)&cx.bp, &bpcap_bytes, (size_t)chunk * per, 1, &cx.owned)) return 2;
+    cx.bp_cap = bpcap_bytes;
+    size_t sc = cx.seq_cap;
+    if ((size_t)chunk > sc) {
+        size_t sc2 = cx.seq_cap;
+        if (grow(&cx.send, &sc, (size_t)chunk, sizeof(int32_t), &cx.owned)) return 2;
+        if (grow(&cx.ov, &sc2, (size_t)chunk, sizeof(int32_t), &cx.owned)) return 2;
+        cx.seq_cap = sc;
+    }
+    const int n1 = (margin > 0 && pivot + margin < xtq::kSteps) ? pivot + margin : xtq::kSteps;
+    const uint16_t* lut = cx.lut16[code];
+    for (int c0 = 0; c0 < nseq; c0 += chunk) {
+        const int n = (nseq - c0) < chunk ? (nseq - c0) : chunk;
+        const float* x = dX + (size_t)c0 * xtq::kSteps;
+        int T = xtq::forward_group(K, n, cx.ncu);
+        if (const char* g = getenv("XTQ_VIT_GROUP")) {
+            // Test hook: force the sequences-per-workgroup (1, 2 or 4),
+            // clamped to what the LDS footprint for K allows.
+            const int want = atoi(g);
+            const int cap = xtq::forward_group(K, 1 << 30, 1);
+            if (want == 1 || want == 2 || want == 4) T = want < cap ? want : cap;
+        }
+        hipError_t e;
+        e = xtq::launch_forward(K, x, n, lut, 1, pivot, n1, pivot, nullptr, cx.bp, cx.send,
+                                cx.err, T, s);
+        if (e == hipSuccess)
+            e = xtq::launch_traceback(K, cx.bp, n, cx.send, 1, pivot, n1, cx.ov, nullptr,
+                                      nullptr, s);
+        if (e == hipSuccess)
+            e = xtq::launch_forward(K, x, n, lut, 2, 0, xtq::kSteps, 0, cx.ov, cx.bp, cx.send,
+                                    cx.err, T, s);
+        if (e == hipSuccess)
+            e = xtq::launch_traceback(
+                K, cx.bp, n, cx.send, 2, 0, xtq::kSteps, nullptr,
+                d_states ? d_states + (size_t)c0 * xtq::kSteps : nullptr,
+                d_trellis ? d_trellis + (size_t)c0 * 16 * K : nullptr, s);
+        if (e != hipSuccess) {
+            fprintf(stderr, "xtq_vit run: %s\n", hipGetErrorString(e));
+            return 4;
+        }
+    }
+    uint32_t herr = 0;
+    if (hipMemcpyAsync(&herr, cx.err, sizeof(herr), hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess) {
+        fprintf(stderr, "xtq_vit run: %s\n", hipGetErrorString(hipGetLastError()));
+        return 4;
+    }
+    if (herr) {
+        (void)hipMemset(cx.err, 0, sizeof(uint32_t));
+        fprintf(stderr, "xtq_vit: NaN target\n");
+        return 11;
+    }
+    return 0;
+}
+
+// Host-pointer tail-bite: stage X, run, copy the states back.
+int run_host(const float* X, int nseq, int K, Code code, int margin, int pivot,
+             int32_t* out) {
+    if (!X || !out) return 12;
+    read_env();
+    int rc = check_common(nseq, K, margin, pivot);
+    if (rc) return rc;
+    int dev = 0, prev = 0;
+    rc = host_entry_device(&dev);
+    if (rc) return rc;
+    if (hipGetDevice(&prev) != hipSuccess) return 1;
+    if (dev != prev && hipSetDevice(dev) != hipSuccess) return 1;
+    rc = dev_init(dev);
+    if (!rc) {
+        DevCtx& cx = g_dev[dev];
+        const size_t add = (size_t)nseq > cx.host_cap
+                               ? ((size_t)nseq - cx.host_cap) * 2 * xtq::kSteps * 4 : 0;
+        if (cx.owned + add > g_maxbytes) {
+            fprintf(stderr, "xtq_vit: nseq %d over XTQ_VIT_MAXBYTES\n", nseq);
+            rc = 5;
+        }
+        size_t c1 = cx.host_cap, c2 = cx.host_cap;
+        if (!rc && (size_t)nseq > cx.host_cap) {
+            if (grow(&cx.hx, &c1, (size_t)nseq * xtq::kSteps, sizeof(float), &cx.owned) ||
+                grow(&cx.hs, &c2, (size_t)nseq * xtq::kSteps, sizeof(int32_t), &cx.owned)) {
+                rc = 2;
+            } else {
+                cx.host_cap = nseq;
+            }
+        }
+        if (!rc && hipMemcpy(cx.hx, X, (size_t)nseq * xtq::kSteps * 4, hipMemcpyHostToDevice) !=
+                       hipSuccess)
+            rc = 4;
+        if (!rc) rc = run_tailbite(cx, cx.hx, nseq, K, code, margin, pivot, cx.hs, nullptr, 0);
+        if (!rc && hipMemcpy(out, cx.hs, (size_t)nseq * xtq::kSteps * 4, hipMemcpyDeviceToHost) !=
+                       hipSuccess)
+            rc = 4;
+    }
+    if (dev != prev) (void)hipSetDevice(prev);
+    return rc;
+}
+
+}  // namespace
+
+extern "C" {
+
+int xtq_vit_init(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    read_env();
+    int dev = 0;
+    int rc = host_entry_device(&dev);
+    if (rc) return rc;
+    int prev = 0;
+    if (hipGetDevice(&prev) != hipSuccess) return 1;
+    if (dev != prev && hipSetDevice(dev) != hipSuccess) return 1;
+    rc = dev_init(dev);
+    if (!rc) {
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, dev) == hipSuccess)
+            fprintf(stderr, "xtq_vit: device %d %s (%s), %d CUs\n", dev, p.name, p.gcnArchName,
+                    p.multiProcessorCount);
+        fprintf(stderr, "xtq_vit: bounds nseq<=%lld devbytes<=%zu scratch=%zu\n", g_maxseq,
+                g_maxbytes, g_scratch);
+    }
+    if (dev != prev) (void)hipSetDevice(prev);
+    return rc;
+}
+
+int xtq_vit_run(const float* X, int nseq, const char* code, int margin, int pivot,
+                int32_t* out) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!code) return 12;
+    if (!strcmp(code, "ih2x2")) {
+        fprintf(stderr, "xtq_vit: code ih2x2 (V=2) is not supported\n");
+        return 8;
+    }
+    if (strcmp(code, "mul1p") && strcmp(code, "mul1") && strcmp(code, "mul1t")) {
+        fprintf(stderr, "xtq_vit: unknown code %s\n", code);
+        return 8;
+    }
+    return run_host(X, nseq, 4, kMul1, margin, pivot, out);
+}
+
+int xtq_vit_run_k(const float* X, int nseq, int K, const char* code, int margin, int pivot,
+                  int32_t* out) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    Code c;
+    int rc = parse_code(code, &c);
+    if (rc) return rc;
+    return run_host(X, nseq, K, c, margin, pivot, out);
+}
+
+int xtq_vit_tailbite_dev(const float* dX, int nseq, int K, const char* code, int margin,
+                         int pivot, int32_t* d_states, int16_t* d_trellis, void* stream) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!dX || (!d_states && !d_trellis)) return 12;
+    Code c;
+    int rc = parse_code(code, &c);
+    if (rc) return rc;
+    read_env();
+    rc = check_common(nseq, K, margin, pivot);
+    if (rc) return rc;
+    int dev = 0;
+    if (current_device(&dev)) return 1;
+    rc = dev_init(dev);
+    if (rc) return rc;
+    return run_tailbite(g_dev[dev], dX, nseq, K, c, margin, pivot, d_states, d_trellis,
+                        (hipStream_t)stream);
+}
+
+int xtq_trellis_decode_dev(const int16_t* d_trellis, int tk, int tn, int K, const char* code,
+                           float* d_out_f32, uint16_t* d_out_f16, void* stream) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!d_trellis || (!d_out_f32 && !d_out_f16)) return 12;
+    if (K < 2 || K > 7) return 9;
+    if (tk <= 0 || tn <= 0 || (long long)tk * tn > (1LL << 31) - 1) return 6;
+    Code c;
+    int rc = parse_code(code, &c);
+    if (rc) return rc;
+    int dev = 0;
+    if (current_device(&dev)) return 1;
+    rc = dev_init(dev);
+    if (rc) return rc;
+    hipError_t e = xtq::launch_decode(K, d_trellis, tk, tn, g_dev[dev].lut16[c], d_out_f32,
+                                      d_out_f16, (hipStream_t)stream);
+    if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+    if (e != hipSuccess) {
+        fprintf(stderr, "xtq_vit decode: %s\n", hipGetErrorString(e));
+        return 4;
+    }
+    return 0;
+}
+
+int xtq_trellis_pack_dev(const int32_t* d_states, int nt, int K, int16_t* d_trellis,
+                         void* stream) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!d_states || !d_trellis) return 12;
+    if (K < 2 || K > 7) return 9;
+    if (nt <= 0) return 6;
+    hipError_t e = xtq::launch_pack(K, d_states, nt, d_trellis, (hipStream_t)stream);
+    if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+    if (e != hipSuccess) {
+        fprintf(stderr, "xtq_vit pack: %s\n", hipGetErrorString(e));
+        return 4;
+    }
+    return 0;
+}
+
+int xtq_trellis_unpack_dev(const int16_t* d_trellis, int nt, int K, int32_t* d_states,
+                           void* stream) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!d_states || !d_trellis) return 12;
+    if (K < 2 || K > 7) return 9;
+    if (nt <= 0) return 6;
+    hipError_t e = xtq::launch_unpack(K, d_trellis, nt, d_states, (hipStream_t)stream);
+    if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+    if (e != hipSuccess) {
+        fprintf(stderr, "xtq_vit unpack: %s\n", hipGetErrorString(e));
+        return 4;
+    }
+    return 0;
+}
+
+int xtq_vit_get_lut(const char* code, float* out) {
+    if (!out) return 12;
+    Code c;
+    int rc = parse_code(code, &c);
+    if (rc) return rc;
+    std::vector<uint16_t> h(65536);
+    make_lut16(c, h.data());
+    for (int s = 0; s < 65536; ++s) out[s] = (float)half_to_double(h[s]);
+    return 0;
+}
+
+int64_t xtq_vit_scratch_per_seq(int K) {
+    if (K < 2 || K > 7) return -1;
+    return (int64_t)xtq::bp_tile_bytes(K);
+}
+
+const char* xtq_vit_strerror(int rc) {
+    switch (rc) {
+        case 0: return "ok";
+        case 1: return "initialisation failed";
+        case 2: return "device allocation failed";
+        case 3: return "XTQ_VIT_DEVIDX names no device";
+        case 4: return "HIP runtime error during a run";
+        case 5: return "request exceeds XTQ_VIT_MAXBYTES";
+        case 6: return "sequence count out of range";
+        case 8: return "unsupported code";
+        case 9: return "unsupported K";
+        case 10: return "pivot or margin out of range";
+        case 11: return "NaN target";
+        case 12: return "null pointer argument";
+        default: return "unknown status";
+    }
+}
+
+}  // extern "C"

@@ -1,0 +1,63 @@
+// viterbi_kernels.h -- internal launch interface of the gfx950 trellis kernels.
+//
+// Not part of the C-ABI: the exported entry points live in exl3_vit_capi.hip
+// and are declared in include/exl3_vit.h.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+namespace xtq {
+
+// Threads per forward workgroup; one workgroup advances T (1, 2 or 4)
+// 256-step sequences in lockstep, 64 trellis states per thread per sequence.
+constexpr int kFwdThreads = 1024;
+// Threads per traceback workgroup.
+constexpr int kTbThreads = 256;
+// Number of trellis steps per sequence (16x16 tile).
+constexpr int kSteps = 256;
+// Backpointer slots stored per sequence: steps 1..255 of a pass.
+constexpr int kSlots = kSteps - 1;
+
+// Bytes of backpointers one sequence writes per step, for K bits per weight.
+size_t bp_step_bytes(int K);
+// Bytes of backpointer scratch one sequence needs for a whole pass.
+inline size_t bp_tile_bytes(int K) { return (size_t)kSlots * bp_step_bytes(K); }
+
+// Sequences per forward workgroup chosen for a launch of nseq sequences on a
+// device with ncu compute units (LDS bounds it by K; small launches use 1).
+int forward_group(int K, int nseq, int ncu);
+
+// Forward DP of one pass for nseq sequences.
+//   X       [nseq][256] fp32 targets (device)
+//   lut16   [65536] fp16 bit patterns of the codebook (device)
+//   pass    1: free start, rolled by pivot, nsteps = n1;  2: pinned to ov_in
+//   store_lo first step index whose backpointers are kept
+//   bp      backpointer scratch, bp_tile_bytes(K) per sequence (device)
+//   send    [nseq] final state of the pass (device, out)
+//   err     device word, OR-ed with 1 when a target is NaN
+hipError_t launch_forward(int K, const float* X, int nseq, const uint16_t* lut16,
+                          int pass, int pivot, int nsteps, int store_lo,
+                          const int32_t* ov_in, void* bp, int32_t* send,
+                          uint32_t* err, int group, hipStream_t stream);
+
+// Traceback of one pass.  Pass 1 writes ov_out[q] = s_pivot >> K.  Pass 2
+// writes the 256 states (states, nullable) and/or the packed EXL3 trellis
+// (trellis [nseq][16K] int16, nullable).
+hipError_t launch_traceback(int K, const void* bp, int nseq, const int32_t* send,
+                            int pass, int pivot, int nsteps, int32_t* ov_out,
+                            int32_t* states, int16_t* trellis,
+                            hipStream_t stream);
+
+// Trellis decode: int16 [tk][tn][16K] -> [16tk][16tn] (fp32 or fp16 bits).
+hipError_t launch_decode(int K, const int16_t* trellis, int tk, int tn,
+                         const uint16_t* lut16, float* out_f32,
+                         uint16_t* out_f16, hipStream_t stream);
+
+// Pack / unpack between int32 states [nt][256] and int16 trellis [nt][16K].
+hipError_t launch_pack(int K, const int32_t* states, int nt, int16_t* trellis,
+                       hipStream_t stream);
+hipError_t launch_unpack(int K, const int16_t* trellis, int nt, int32_t* states,
+                         hipStream_t stream);
+
+}  // namespace xtq

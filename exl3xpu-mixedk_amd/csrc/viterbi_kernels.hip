@@ -1,0 +1,587 @@
+// viterbi_kernels.hip -- gfx950 kernels for the EXL3 tail-biting trellis encoder.
+//
+// Contract (bit-exact with the reference torch Viterbi, quantize.py:218-354):
+//   emit      e[s] = fl(fl(f[s] - x)^2)           (no FMA contraction)
+//   step      c_i[s] = fl(e_i[s] + b_i[s >> K])
+//   reduce    b_{i+1}[j] = min_w c_i[j + w*SP], lowest w on ties
+//   end       lowest state index among equal minima (free end); pinned end
+//             keeps only states with s mod SP == ov
+//
+// Work decomposition (16-bit state, K bits per step, NC = 2^K predecessors,
+// SP = 2^(16-K) groups):
+//   * one 1024-thread workgroup (16 waves, one per CU at 4 waves/SIMD)
+//     advances T = 1, 2 or 4 sequences in lockstep;
+//   * thread t owns the C = SP/1024 consecutive groups j = t*C .. t*C+C-1
+//     (K=7: half of group t/2) and the candidate states of each,
+//     s = j + w*SP, i.e. 64 states per thread for every K; their codebook
+//     values stay in 32 VGPRs as packed fp16 pairs for the whole kernel
+//     (every supported codebook is fp16-exact), are shared by the T
+//     sequences and are widened exactly inside v_fma_mix_f32;
+//   * the per-group minima b (SP floats per sequence) are the only state
+//     carried between steps; they live in LDS, double buffered, one barrier
+//     per step for all T sequences;
+//   * min and first-index argmin fold into one v_min_f64 per candidate: the
+//     cost (non-negative fp32) is the high dword and the predecessor index
+//     the low dword of a 64-bit key, so the fp64 order of the keys is the
+//     lexicographic order (cost, index) -- the reference's tie rule;
+//   * backpointers are K bits per group, packed per thread and written
+//     coalesced to HBM; a separate traceback kernel stages them through LDS.
+#include "viterbi_kernels.h"
+
+#pragma clang fp contract(off)
+
+namespace xtq {
+namespace {
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+template <int K>
+struct Geom {
+    static constexpr int NC = 1 << K;                 // predecessors per group
+    static constexpr int SP = 1 << (16 - K);          // groups
+    static constexpr int Q = 1 << (16 - 2 * K);       // NC x NC blocks per step
+    static constexpr bool HALF = (SP < kFwdThreads);  // K=7: two lanes per group
+    static constexpr int C = HALF ? 1 : SP / kFwdThreads;  // groups per thread
+    static constexpr int W = HALF ? NC / 2 : NC;      // candidates per group/thread
+    static constexpr int NCH = W < 16 ? W : 16;       // candidates per chunk
+    static constexpr int NCHUNK = W / NCH;
+    static constexpr int NB = C > NC ? C / NC : 1;    // blocks per thread
+    static constexpr int CB = C / NB;                 // groups per block
+    static constexpr int NSTATE = C * W;              // states per thread
+    static constexpr int BITS = C * K;                // backpointer bits/thread
+    static constexpr int UNIT = HALF ? 1 : BITS <= 8 ? 1 : BITS <= 16 ? 2 : 4;
+    // Bytes per step: one unit per thread, or one byte per group when two
+    // lanes share a group.
+    static constexpr int BPSTEP = HALF ? SP : kFwdThreads * UNIT;
+    static_assert(NSTATE == 64, "64 states per thread");
+    static_assert(BITS <= 32, "backpointer unit");
+    static_assert(BPSTEP % 16 == 0, "staging granularity");
+};
+
+template <int N> struct UnitT;
+template <> struct UnitT<1> { typedef uint8_t type; };
+template <> struct UnitT<2> { typedef uint16_t type; };
+template <> struct UnitT<4> { typedef uint32_t type; };
+
+// 64-bit key: high dword = cost bits, low dword = tag (index in the low byte).
+__device__ __forceinline__ double key_of(uint32_t lo, float c) {
+    return __builtin_bit_cast(double,
+                              (uint64_t)lo | ((uint64_t)__float_as_uint(c) << 32));
+}
+__device__ __forceinline__ float key_cost(double k) {
+    return __uint_as_float((uint32_t)(__builtin_bit_cast(uint64_t, k) >> 32));
+}
+__device__ __forceinline__ uint32_t key_lo(double k) {
+    return (uint32_t)__builtin_bit_cast(uint64_t, k);
+}
+// Keys are never NaN (the high dword is a non-negative fp32 cost <= +inf) and
+// IEEE min needs no canonicalisation here, so issue v_min_f64 directly.
+__device__ __forceinline__ double kmin(double a, double b) {
+    double r;
+    asm("v_min_f64 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
+__device__ __forceinline__ double kmin_xor(double k, int m) {
+    const uint32_t lo = key_lo(k), hi = __float_as_uint(key_cost(k));
+    const uint32_t plo = __shfl_xor(lo, m), phi = __shfl_xor(hi, m);
+    return kmin(k, key_of(plo, __uint_as_float(phi)));
+}
+
+// Backpointer of group j in one step's row.
+template <int K>
+__device__ __forceinline__ int bp_lookup(const uint8_t* row, int j) {
+    using G = Geom<K>;
+    if constexpr (G::HALF) {
+        return row[j];
+    } else {
+        typedef typename UnitT<G::UNIT>::type unit_t;
+        const unit_t u = ((const unit_t*)row)[j / G::C];
+        return (int)((u >> ((j % G::C) * K)) & (unit_t)(G::NC - 1));
+    }
+}
+
+// --------------------------------------------------------------- forward DP
+// One workgroup = 1024 threads = T sequences processed in lockstep (the
+// codebook registers are shared by the T sequences; one barrier per step).
+template <int K, int T>
+__global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
+    const float* __restrict__ X, int nseq, const uint16_t* __restrict__ lut16, int pass,
+    int pivot, int nsteps, int store_lo, const int32_t* __restrict__ ov_in,
+    uint8_t* __restrict__ bp, int32_t* __restrict__ send, uint32_t* __restrict__ err,
+    float one) {
+    using G = Geom<K>;
+    __shared__ __attribute__((aligned(16))) float bbuf[T][2][G::SP];
+    __shared__ float xs[T][kSteps];
+    __shared__ int32_t ovs[T];
+    __shared__ double red[kFwdThreads / 64];
+
+    const int tid = threadIdx.x;
+    const int q0 = blockIdx.x * T;
+    const int ntile = (nseq - q0) < T ? (nseq - q0) : T;   // sequences in this group
+    if (tid < T * kSteps) {
+        const int tt = tid / kSteps, e = tid % kSteps;
+        float v = 0.0f;
+        if (tt < ntile) {
+            v = X[(size_t)(q0 + tt) * kSteps + e];
+            if (v != v) atomicOr(err, 1u);
+        }
+        xs[tt][e] = v;
+    }
+    if (tid < T) ovs[tid] = (pass == 2 && tid < ntile) ? ov_in[q0 + tid] : -1;
+
+    // Owned groups and candidates: groups j_c = jbase + c, candidate w of a
+    // group is state j_c + (wbase + w) * SP; local index l = c*W + w.
+    const int jbase = G::HALF ? (tid >> 1) : tid * G::C;
+    const int wbase = G::HALF ? (tid & 1) * G::W : 0;
+    h2_t fh[G::NSTATE / 2];
+#pragma unroll
+    for (int l = 0; l < G::NSTATE / 2; ++l) {
+        const int l0 = 2 * l, l1 = 2 * l + 1;
+        const int s0 = jbase + l0 / G::W + (wbase + l0 % G::W) * G::SP;
+        const int s1 = jbase + l1 / G::W + (wbase + l1 % G::W) * G::SP;
+        h2_t v;
+        v.x = __builtin_bit_cast(_Float16, lut16[s0]);
+        v.y = __builtin_bit_cast(_Float16, lut16[s1]);
+        fh[l] = v;
+    }
+    // Per-lane key tags: distinct per lane so they stay in VGPRs next to the
+    // cost they are paired with; the low byte is the candidate index.
+    uint32_t tag[G::NCH];
+#pragma unroll
+    for (int w = 0; w < G::NCH; ++w) tag[w] = ((uint32_t)tid << 8) | (uint32_t)(wbase + w);
+    __syncthreads();
+
+    // Start mask b_0: 0 everywhere (free) or 0 only at group ov (pinned).
+    for (int tt = 0; tt < T; ++tt) {
+        const int ov = ovs[tt];
+        if (!G::HALF || (tid & 1) == 0) {
+#pragma unroll
+            for (int c = 0; c < G::C; ++c) {
+                const int j = jbase + c;
+                bbuf[tt][0][j] = (ov < 0 || j == ov) ? 0.0f : __builtin_inff();
+            }
+        }
+    }
+    __syncthreads();
+
+    const int a0 = jbase >> K;  // first NC x NC block this thread reads
+    for (int i = 0; i < nsteps; ++i) {
+        const int u = (pass == 1) ? ((i - pivot) & (kSteps - 1)) : i;
+#pragma unroll 1
+        for (int tt = 0; tt < ntile; ++tt) {
+            // Keep the fp16 codebook pairs opaque per sequence-step so the
+            // widening stays inside v_fma_mix_f32 instead of being hoisted
+            // into fp32 VGPRs.
+#pragma unroll
+            for (int l = 0; l < G::NSTATE / 2; ++l) asm volatile("" : "+v"(fh[l]));
+            const int q = q0 + tt;
+            const float negx = -__int_as_float(
+                __builtin_amdgcn_readfirstlane(__float_as_int(xs[tt][u])));
+            const float* bcur = bbuf[tt][i & 1];
+
+            double run[G::C];
+#pragma unroll
+            for (int qc = 0; qc < G::NCHUNK; ++qc) {
+                float B[G::NB][G::NCH];
+#pragma unroll
+                for (int w = 0; w < G::NCH; ++w) {
+                    const float* src = bcur + a0 + (wbase + qc * G::NCH + w) * G::Q;
+                    if constexpr (G::NB == 4) {
+                        const float4 v = *(const float4*)src;
+                        B[0][w] = v.x; B[1][w] = v.y; B[2][w] = v.z; B[3][w] = v.w;
+                    } else {
+                        B[0][w] = src[0];
+                    }
+                }
+#pragma unroll
+                for (int c = 0; c < G::C; ++c) {
+                    const int blk = c / G::CB;
+                    double kk[G::NCH];
+#pragma unroll
+                    for (int w = 0; w < G::NCH; ++w) {
+                        const int l = c * G::W + qc * G::NCH + w;
+                        const float fv = (l & 1) ? (float)fh[l >> 1].y : (float)fh[l >> 1].x;
+                        const float d = __builtin_fmaf(fv, one, negx);  // == fl(f - x)
+                        const float e = d * d;
+                        kk[w] = key_of(tag[w], e + B[blk][w]);
+                    }
+#pragma unroll
+                    for (int st = 1; st < G::NCH; st *= 2)
+#pragma unroll
+                        for (int w = 0; w < G::NCH; w += 2 * st) kk[w] = kmin(kk[w], kk[w + st]);
+                    if (qc == 0) {
+                        run[c] = kk[0];
+                    } else {
+                        const double kq = key_of(key_lo(kk[0]) + (uint32_t)(qc * G::NCH),
+                                                 key_cost(kk[0]));
+                        run[c] = kmin(run[c], kq);
+                    }
+                }
+            }
+            if constexpr (G::HALF) run[0] = kmin_xor(run[0], 1);  // merge the two halves
+
+            uint8_t* bpq = bp + (size_t)q * ((size_t)kSlots * G::BPSTEP);
+            if (i + 1 < nsteps) {
+                float* bnext = bbuf[tt][(i + 1) & 1] + jbase;
+                if constexpr (G::C % 4 == 0) {
+#pragma unroll
+                    for (int c = 0; c < G::C; c += 4)
+                        *(float4*)(bnext + c) =
+                            make_float4(key_cost(run[c]), key_cost(run[c + 1]),
+                                        key_cost(run[c + 2]), key_cost(run[c + 3]));
+                } else if constexpr (G::C == 2) {
+                    *(float2*)bnext = make_float2(key_cost(run[0]), key_cost(run[1]));
+                } else {
+                    if (!G::HALF || (tid & 1) == 0) bnext[0] = key_cost(run[0]);
+                }
+                if (i >= store_lo) {
+                    if constexpr (G::HALF) {
+                        if ((tid & 1) == 0)
+                            bpq[(size_t)i * G::BPSTEP + jbase] = (uint8_t)(key_lo(run[0]) & 0x7F);
+                    } else {
+                        typedef typename UnitT<G::UNIT>::type unit_t;
+                        uint32_t bits = 0;
+#pragma unroll
+                        for (int c = 0; c < G::C; ++c)
+                            bits |= (key_lo(run[c]) & (uint32_t)(G::NC - 1)) << (c * K);
+                        *(unit_t*)(bpq + (size_t)i * G::BPSTEP + (size_t)tid * G::UNIT) =
+                            (unit_t)bits;
+                    }
+                }
+            } else if (pass == 2) {
+                // Pinned end: the allowed final states are exactly group ov's
+                // candidates, so s_end = ov + argmin_w * SP.  When even the
+                // best allowed cost is +inf, cost + mask is +inf everywhere
+                // and the reference's argmin returns state 0
+                // (quantize.py:298-306).
+                const int ov = ovs[tt];
+#pragma unroll
+                for (int c = 0; c < G::C; ++c)
+                    if (jbase + c == ov && (!G::HALF || (tid & 1) == 0)) {
+                        const float m = key_cost(run[c]);
+                        send[q] = (m == __builtin_inff())
+                                      ? 0
+                                      : ov + (int)(key_lo(run[c]) & (uint32_t)(G::NC - 1)) * G::SP;
+                    }
+            } else {
+                // Free end: lowest state index among the minimum costs.  The
+                // first argmin of a group is its lowest state; across groups
+                // compare (cost, state) as one key.
+                double best = 0.0;
+#pragma unroll
+                for (int c = 0; c < G::C; ++c) {
+                    const uint32_t s = (uint32_t)(jbase + c) +
+                                       (key_lo(run[c]) & (uint32_t)(G::NC - 1)) * (uint32_t)G::SP;
+                    const double kc = key_of(s, key_cost(run[c]));
+                    best = (c == 0) ? kc : kmin(best, kc);
+                }
+#pragma unroll
+                for (int m = 32; m >= 1; m >>= 1) best = kmin_xor(best, m);
+                if ((tid & 63) == 0) red[tid >> 6] = best;
+                __syncthreads();
+                if (tid == 0) {
+                    double b = red[0];
+#pragma unroll
+                    for (int wv = 1; wv < kFwdThreads / 64; ++wv) b = kmin(b, red[wv]);
+                    send[q] = (int)key_lo(b);
+                }
+                __syncthreads();
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------- traceback
+template <int K>
+__global__ __launch_bounds__(kTbThreads) void tb_kernel(
+    const uint8_t* __restrict__ bp, const int32_t* __restrict__ send, int pass,
+    int pivot, int nsteps, int32_t* __restrict__ ov_out,
+    int32_t* __restrict__ states, int16_t* __restrict__ trellis) {
+    using G = Geom<K>;
+    constexpr int STAGE = 32768;
+    constexpr int CH = STAGE / G::BPSTEP;  // slots per staged chunk
+    __shared__ uint4 stage[STAGE / 16];
+    __shared__ int32_t st[kSteps];
+    __shared__ int32_t cur;
+
+    const int q = blockIdx.x, tid = threadIdx.x;
+    const uint8_t* bpq = bp + (size_t)q * ((size_t)kSlots * G::BPSTEP);
+    const int stop = (pass == 1) ? pivot : 0;
+    if (tid == 0) {
+        cur = send[q] & 0xFFFF;
+        if (pass == 2) st[nsteps - 1] = cur;
+    }
+    // Step i (s_i -> s_{i-1}) reads slot i-1; slots stop .. nsteps-2.
+    for (int hi = nsteps - 2; hi >= stop; ) {
+        const int lo = (hi - CH + 1 > stop) ? hi - CH + 1 : stop;
+        const int n16 = (hi - lo + 1) * (G::BPSTEP / 16);
+        const uint4* src = (const uint4*)(bpq + (size_t)lo * G::BPSTEP);
+        __syncthreads();
+        for (int k = tid; k < n16; k += kTbThreads) stage[k] = src[k];
+        __syncthreads();
+        if (tid == 0) {
+            int s = cur;
+            for (int sl = hi; sl >= lo; --sl) {
+                const int j = (s >> K) & (G::SP - 1);
+                const uint8_t* row = (const uint8_t*)stage + (size_t)(sl - lo) * G::BPSTEP;
+                s = j + bp_lookup<K>(row, j) * G::SP;
+                if (pass == 2) st[sl] = s;
+            }
+            cur = s;
+        }
+        hi = lo - 1;
+    }
+    __syncthreads();
+    if (pass == 1) {
+        if (tid == 0) ov_out[q] = cur >> K;
+        return;
+    }
+    if (states) {
+        for (int t = tid; t < kSteps; t += kTbThreads) states[(size_t)q * kSteps + t] = st[t];
+    }
+    if (trellis) {
+        // Symbol t = s_t mod 2^K at stream bits [tK, (t+1)K), MSB first;
+        // 32-bit words MSB first, stored as int16 halves, low half first.
+        for (int wd = tid; wd < 8 * K; wd += kTbThreads) {
+            uint32_t word = 0;
+            for (int bb = 0; bb < 32; ++bb) {
+                const int b = wd * 32 + bb, t = b / K, k = b - t * K;
+                word |= (((uint32_t)st[t] >> (K - 1 - k)) & 1u) << (31 - bb);
+            }
+            int16_t* o = trellis + (size_t)q * 16 * K + 2 * wd;
+            o[0] = (int16_t)(uint16_t)(word & 0xFFFFu);
+            o[1] = (int16_t)(uint16_t)(word >> 16);
+        }
+    }
+}
+
+// ------------------------------------------------- decode / pack / unpack
+// tensor_core_perm (quantize.py:101-118): element t -> row-major 16x16 index.
+__device__ __forceinline__ int tc_perm(int t) {
+    const int g = t >> 3, e = t & 7;
+    const int r0 = (g & 3) * 2, c0 = g >> 2;
+    const int rr = (e & 1) + ((e & 2) ? 8 : 0);
+    const int cc = (e & 4) ? 8 : 0;
+    return (r0 + rr) * 16 + c0 + cc;
+}
+
+// 16-bit circular window of the 256K-bit stream ending at bit (t+1)K - 1.
+template <int K>
+__device__ __forceinline__ uint32_t window_state(const uint32_t* words, int t) {
+    constexpr int NB = 256 * K;
+    int b = t * K + K - 16;
+    if (b < 0) b += NB;
+    uint32_t v = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        int bb = b + k;
+        if (bb >= NB) bb -= NB;
+        v = (v << 1) | ((words[bb >> 5] >> (31 - (bb & 31))) & 1u);
+    }
+    return v;
+}
+
+template <int K>
+__global__ __launch_bounds__(256) void decode_kernel(
+    const int16_t* __restrict__ trellis, int tn, const uint16_t* __restrict__ lut16,
+    float* __restrict__ out_f32, uint16_t* __restrict__ out_f16) {
+    __shared__ uint32_t words[8 * K];
+    const int tile = blockIdx.x, t = threadIdx.x;
+    const uint32_t* src = (const uint32_t*)(trellis + (size_t)tile * 16 * K);
+    if (t < 8 * K) words[t] = src[t];  // int16 pair [lo, hi] == little-endian u32
+    __syncthreads();
+    const uint32_t s = window_state<K>(words, t);
+    const int p = tc_perm(t);
+    const int a = tile / tn, b = tile - a * tn;
+    const size_t n = (size_t)tn * 16;
+    const size_t idx = (size_t)(16 * a + (p >> 4)) * n + 16 * b + (p & 15);
+    const uint16_t h = lut16[s];
+    if (out_f32) out_f32[idx] = (float)__builtin_bit_cast(_Float16, h);
+    if (out_f16) out_f16[idx] = h;
+}
+
+template <int K>
+__global__ __launch_bounds__(256) void unpack_kernel(const int16_t* __restrict__ trellis,
+                                                     int32_t* __restrict__ states) {
+    __shared__ uint32_t words[8 * K];
+    const int tile = blockIdx.x, t = threadIdx.x;
+    const uint32_t* src = (const uint32_t*)(trellis + (size_t)tile * 16 * K);
+    if (t < 8 * K) words[t] = src[t];
+    __syncthreads();
+    states[(size_t)tile * kSteps + t] = (int32_t)window_state<K>(words, t);
+}
+
+template <int K>
+__global__ __launch_bounds__(64) void pack_kernel(const int32_t* __restrict__ states,
+                                                  int16_t* __restrict__ trellis) {
+    const int tile = blockIdx.x, wd = threadIdx.x;
+    if (wd >= 8 * K) return;
+    const int32_t* st = states + (size_t)tile * kSteps;
+    uint32_t word = 0;
+    for (int bb = 0; bb < 32; ++bb) {
+        const int b = wd * 32 + bb, t = b / K, k = b - t * K;
+        word |= (((uint32_t)st[t] >> (K - 1 - k)) & 1u) << (31 - bb);
+    }
+    int16_t* o = trellis + (size_t)tile * 16 * K + 2 * wd;
+    o[0] = (int16_t)(uint16_t)(word & 0xFFFFu);
+    o[1] = (int16_t)(uint16_t)(word >> 16);
+}
+
+template <template <int> class F, typename... A>
+hipError_t dispatch_k(int K, A... a) {
+    switch (K) {
+        case 2: return F<2>::run(a...);
+        case 3: return F<3>::run(a...);
+        case 4: return F<4>::run(a...);
+        case 5: return F<5>::run(a...);
+        case 6: return F<6>::run(a...);
+        case 7: return F<7>::run(a...);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// Largest group size whose LDS footprint (2 x SP floats + 1 KiB per
+// sequence) fits one CU's 160 KiB.
+template <int K>
+constexpr int max_group() {
+    constexpr size_t per = 2 * sizeof(float) * Geom<K>::SP + 1024 + 16;
+    return (4 * per + 512 <= 160 * 1024) ? 4 : (2 * per + 512 <= 160 * 1024) ? 2 : 1;
+}
+
+template <int K>
+struct FwdL {
+    static hipError_t run(const float* X, int nseq, const uint16_t* lut16, int pass,
+                          int pivot, int nsteps, int store_lo, const int32_t* ov_in,
+                          void* bp, int32_t* send, uint32_t* err, int group,
+                          hipStream_t s) {
+        const int T = group <= 1 ? 1 : group <= 2 ? 2 : 4;
+        if (T > max_group<K>()) return hipErrorInvalidValue;
+        const int nwg = (nseq + T - 1) / T;
+        if (T == 1)
+            hipLaunchKernelGGL((fwd_kernel<K, 1>), dim3(nwg), dim3(kFwdThreads), 0, s, X,
+                               nseq, lut16, pass, pivot, nsteps, store_lo, ov_in,
+                               (uint8_t*)bp, send, err, 1.0f);
+        else if constexpr (max_group<K>() >= 2) {
+            if (T == 2)
+                hipLaunchKernelGGL((fwd_kernel<K, 2>), dim3(nwg), dim3(kFwdThreads), 0, s,
+                                   X, nseq, lut16, pass, pivot, nsteps, store_lo, ov_in,
+                                   (uint8_t*)bp, send, err, 1.0f);
+            else if constexpr (max_group<K>() >= 4)
+                hipLaunchKernelGGL((fwd_kernel<K, 4>), dim3(nwg), dim3(kFwdThreads), 0, s,
+                                   X, nseq, lut16, pass, pivot, nsteps, store_lo, ov_in,
+                                   (uint8_t*)bp, send, err, 1.0f);
+        }
+        return hipGetLastError();
+    }
+};
+
+template <int K>
+struct GroupSel {
+    static hipError_t run(int nseq, int ncu, int* out) {
+        // One workgroup per CU is resident; prefer the largest group that
+        // still gives every CU at least two workgroups.
+        int T = max_group<K>();
+        while (T > 1 && (nseq + T - 1) / T < 2 * ncu) T >>= 1;
+        *out = T;
+        return hipSuccess;
+    }
+};
+
+template <int K>
+struct TbL {
+    static hipError_t run(const void* bp, int nseq, const int32_t* send, int pass,
+                          int pivot, int nsteps, int32_t* ov_out, int32_t* states,
+                          int16_t* trellis, hipStream_t s) {
+        hipLaunchKernelGGL(tb_kernel<K>, dim3(nseq), dim3(kTbThreads), 0, s,
+                           (const uint8_t*)bp, send, pass, pivot, nsteps, ov_out, states,
+                           trellis);
+        return hipGetLastError();
+    }
+};
+
+template <int K>
+struct DecL {
+    static hipError_t run(const int16_t* tr, int tk, int tn, const uint16_t* lut16,
+                          float* of, uint16_t* oh, hipStream_t s) {
+        hipLaunchKernelGGL(decode_kernel<K>, dim3(tk * tn), dim3(256), 0, s, tr, tn, lut16,
+                           of, oh);
+        return hipGetLastError();
+    }
+};
+
+template <int K>
+struct PackL {
+    static hipError_t run(const int32_t* st, int nt, int16_t* tr, hipStream_t s) {
+        hipLaunchKernelGGL(pack_kernel<K>, dim3(nt), dim3(64), 0, s, st, tr);
+        return hipGetLastError();
+    }
+};
+
+template <int K>
+struct UnpackL {
+    static hipError_t run(const int16_t* tr, int nt, int32_t* st, hipStream_t s) {
+        hipLaunchKernelGGL(unpack_kernel<K>, dim3(nt), dim3(256), 0, s, tr, st);
+        return hipGetLastError();
+    }
+};
+
+template <int K>
+struct StepBytes {
+    static hipError_t run(size_t* out) {
+        *out = (size_t)Geom<K>::BPSTEP;
+        return hipSuccess;
+    }
+};
+
+}  // namespace
+
+size_t bp_step_bytes(int K) {
+    size_t b = 0;
+    if (dispatch_k<StepBytes>(K, &b) != hipSuccess) return 0;
+    return b;
+}
+
+int forward_group(int K, int nseq, int ncu) {
+    int T = 1;
+    if (dispatch_k<GroupSel>(K, nseq, ncu, &T) != hipSuccess) return 1;
+    return T;
+}
+
+hipError_t launch_forward(int K, const float* X, int nseq, const uint16_t* lut16, int pass,
+                          int pivot, int nsteps, int store_lo, const int32_t* ov_in,
+                          void* bp, int32_t* send, uint32_t* err, int group,
+                          hipStream_t stream) {
+    if (nseq <= 0) return hipSuccess;
+    return dispatch_k<FwdL>(K, X, nseq, lut16, pass, pivot, nsteps, store_lo, ov_in, bp,
+                            send, err, group, stream);
+}
+
+hipError_t launch_traceback(int K, const void* bp, int nseq, const int32_t* send, int pass,
+                            int pivot, int nsteps, int32_t* ov_out, int32_t* states,
+                            int16_t* trellis, hipStream_t stream) {
+    if (nseq <= 0) return hipSuccess;
+    return dispatch_k<TbL>(K, bp, nseq, send, pass, pivot, nsteps, ov_out, states, trellis,
+                           stream);
+}
+
+hipError_t launch_decode(int K, const int16_t* trellis, int tk, int tn, const uint16_t* lut16,
+                         float* out_f32, uint16_t* out_f16, hipStream_t stream) {
+    if (tk <= 0 || tn <= 0) return hipSuccess;
+    return dispatch_k<DecL>(K, trellis, tk, tn, lut16, out_f32, out_f16, stream);
+}
+
+hipError_t launch_pack(int K, const int32_t* states, int nt, int16_t* trellis,
+                       hipStream_t stream) {
+    if (nt <= 0) return hipSuccess;
+    return dispatch_k<PackL>(K, states, nt, trellis, stream);
+}
+
+hipError_t launch_unpack(int K, const int16_t* trellis, int nt, int32_t* states,
+                         hipStream_t stream) {
+    if (nt <= 0) return hipSuccess;
+    return dispatch_k<UnpackL>(K, trellis, nt, states, stream);
+}
+
+}  // namespace xtq

@@ -1,0 +1,175 @@
+"""hip_backend.py -- ctypes binding of libexl3vit.so (include/exl3_vit.h).
+
+The MI355X counterpart of the reference's ESIMD transport
+(quantize.py:441-628): the same C-ABI conventions (int status, caller-owned
+buffers, library-owned scratch), but the encoder runs on torch-ROCm device
+tensors in place, so the LDLQ sweep never round-trips targets through the
+host.  There is no fallback: if the library is missing or the tensors are not
+on a HIP device, the calls raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.environ.get(
+    "XTQ_VIT_LIB",
+    os.path.normpath(os.path.join(_HERE, "..", "lib", "libexl3vit.so")))
+
+_LIB = None
+
+# Codebook names accepted by the library (fp16-exact V=1 codes).
+CODE_NAMES = {"exl3_mul1": "mul1", "exl3_3inst": "3inst", "exl3_mcg": "mcg",
+              "mul1": "mul1", "3inst": "3inst", "mcg": "mcg"}
+
+
+class HipViterbiError(RuntimeError):
+    """A non-zero status from libexl3vit.so."""
+
+    def __init__(self, fn: str, rc: int):
+        msg = lib().xtq_vit_strerror(rc).decode() if _LIB is not None else "?"
+        super().__init__(f"{fn} rc={rc} ({msg})")
+        self.rc = rc
+
+
+def lib():
+    """Load libexl3vit.so once; raises if it has not been built."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"libexl3vit.so not found at {LIB_PATH}; build it with "
+                "`make -C exl3xpu-mixedk_amd` (or __graft_entry__.build())")
+        L = ctypes.CDLL(LIB_PATH)
+        vp, i32, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+        cp = ctypes.c_char_p
+        L.xtq_vit_init.argtypes = []
+        L.xtq_vit_run.argtypes = [vp, i32, cp, i32, i32, vp]
+        L.xtq_vit_run_k.argtypes = [vp, i32, i32, cp, i32, i32, vp]
+        L.xtq_vit_tailbite_dev.argtypes = [vp, i32, i32, cp, i32, i32, vp, vp, vp]
+        L.xtq_trellis_decode_dev.argtypes = [vp, i32, i32, i32, cp, vp, vp, vp]
+        L.xtq_trellis_pack_dev.argtypes = [vp, i32, i32, vp, vp]
+        L.xtq_trellis_unpack_dev.argtypes = [vp, i32, i32, vp, vp]
+        L.xtq_vit_get_lut.argtypes = [cp, vp]
+        L.xtq_vit_scratch_per_seq.argtypes = [i32]
+        L.xtq_vit_scratch_per_seq.restype = i64
+        L.xtq_vit_strerror.argtypes = [i32]
+        L.xtq_vit_strerror.restype = cp
+        for fn in ("xtq_vit_init", "xtq_vit_run", "xtq_vit_run_k", "xtq_vit_tailbite_dev",
+                   "xtq_trellis_decode_dev", "xtq_trellis_pack_dev",
+                   "xtq_trellis_unpack_dev", "xtq_vit_get_lut"):
+            getattr(L, fn).restype = i32
+        _LIB = L
+    return _LIB
+
+
+def _check(fn: str, rc: int):
+    if rc:
+        raise HipViterbiError(fn, rc)
+
+
+def code_name(code: str) -> str:
+    try:
+        return CODE_NAMES[code]
+    except KeyError:
+        raise NotImplementedError(
+            f"code {code!r} has no HIP trellis kernel (supported: "
+            f"{sorted(set(CODE_NAMES))})") from None
+
+
+def _dev_tensor(t: torch.Tensor, dtype: torch.dtype, name: str) -> torch.Tensor:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a HIP device tensor, got {t.device}")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    return t.contiguous()
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def tailbite(X: torch.Tensor, K: int, pivot: int, margin: int, code: str = "mul1",
+             states: bool = True, trellis: bool = False):
+    """Tail-biting encode of X [nseq, 256] fp32 (device).
+
+    Returns (states int32 [nseq, 256] or None, trellis int16 [nseq, 16K] or
+    None), both on X's device.  Bit-exact with quantize_seq_tailbite
+    (quantize.py:323-354) given the same targets, pivot and margin.
+    """
+    X = _dev_tensor(X, torch.float32, "X")
+    if X.dim() != 2 or X.shape[1] != 256:
+        raise ValueError(f"X must be [nseq, 256], got {tuple(X.shape)}")
+    nseq = X.shape[0]
+    st = torch.empty(nseq, 256, dtype=torch.int32, device=X.device) if states else None
+    tr = torch.empty(nseq, 16 * K, dtype=torch.int16, device=X.device) if trellis else None
+    if nseq == 0:
+        return st, tr
+    with torch.cuda.device(X.device):
+        rc = lib().xtq_vit_tailbite_dev(
+            X.data_ptr(), nseq, int(K), code_name(code).encode(), int(margin), int(pivot),
+            st.data_ptr() if st is not None else None,
+            tr.data_ptr() if tr is not None else None, _stream(X.device))
+    _check("xtq_vit_tailbite_dev", rc)
+    return st, tr
+
+
+def decode(trellis: torch.Tensor, K: int, code: str = "mul1",
+           dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """int16 [tk, tn, 16K] (device) -> W_inner [16 tk, 16 tn] (quantize.py:405-415)."""
+    tr = _dev_tensor(trellis, torch.int16, "trellis")
+    tk, tn, w = tr.shape
+    if w != 16 * K:
+        raise ValueError(f"trellis last dim {w} != 16*K = {16 * K}")
+    if dtype not in (torch.float32, torch.float16):
+        raise ValueError("decode dtype must be float32 or float16")
+    out = torch.empty(16 * tk, 16 * tn, dtype=dtype, device=tr.device)
+    if tk == 0 or tn == 0:
+        return out
+    with torch.cuda.device(tr.device):
+        rc = lib().xtq_trellis_decode_dev(
+            tr.data_ptr(), tk, tn, int(K), code_name(code).encode(),
+            out.data_ptr() if dtype == torch.float32 else None,
+            out.data_ptr() if dtype == torch.float16 else None, _stream(tr.device))
+    _check("xtq_trellis_decode_dev", rc)
+    return out
+
+
+def pack(states: torch.Tensor, K: int) -> torch.Tensor:
+    """int32 states [nt, 256] (device) -> int16 trellis [nt, 16K]."""
+    st = _dev_tensor(states, torch.int32, "states")
+    nt = st.shape[0]
+    out = torch.empty(nt, 16 * K, dtype=torch.int16, device=st.device)
+    if nt:
+        with torch.cuda.device(st.device):
+            rc = lib().xtq_trellis_pack_dev(st.data_ptr(), nt, int(K), out.data_ptr(),
+                                            _stream(st.device))
+        _check("xtq_trellis_pack_dev", rc)
+    return out
+
+
+def unpack(trellis: torch.Tensor, K: int) -> torch.Tensor:
+    """int16 trellis [nt, 16K] (device) -> int32 states [nt, 256]."""
+    tr = _dev_tensor(trellis, torch.int16, "trellis").view(-1, 16 * K)
+    nt = tr.shape[0]
+    out = torch.empty(nt, 256, dtype=torch.int32, device=tr.device)
+    if nt:
+        with torch.cuda.device(tr.device):
+            rc = lib().xtq_trellis_unpack_dev(tr.data_ptr(), nt, int(K), out.data_ptr(),
+                                              _stream(tr.device))
+        _check("xtq_trellis_unpack_dev", rc)
+    return out
+
+
+def get_lut(code: str = "mul1") -> torch.Tensor:
+    """fp32 [65536] decode table as the library computes it (host)."""
+    out = torch.empty(65536, dtype=torch.float32)
+    _check("xtq_vit_get_lut", lib().xtq_vit_get_lut(code_name(code).encode(), out.data_ptr()))
+    return out
+
+
+def scratch_per_seq(K: int) -> int:
+    return int(lib().xtq_vit_scratch_per_seq(int(K)))

@@ -1,0 +1,126 @@
+/*
+ * exl3_vit.h -- C-ABI of the MI355X (gfx950) EXL3 trellis encoder library
+ * (libexl3vit.so).
+ *
+ * The library encodes 16x16 weight tiles (256-step sequences) with the QTIP
+ * two-pass tail-biting Viterbi on the 16-bit-state EXL3 trellis, K = 2..7 bits
+ * per weight, and decodes trellis streams back to weights.  Results are
+ * bit-exact with the reference torch path (quantize/quantize.py:218-415).
+ *
+ * Conventions (kept from quantize/viterbi_esimd.cpp:924-1005):
+ *   - every entry point returns an int status, 0 on success; nothing throws
+ *     across the ABI; diagnostics go to stderr;
+ *   - the caller owns all input and output buffers; the library owns a
+ *     per-device, grow-only device scratch it never frees;
+ *   - one caller at a time per process (calls are serialised internally by a
+ *     mutex, but concurrent callers gain nothing);
+ *   - X is [nseq][256] fp32, C-contiguous, one sequence per tile in the
+ *     sequence order x_t = tile[perm[t]] (quantize.py:684-686).
+ *
+ * Status codes:
+ *   0  ok
+ *   1  initialisation failed (no HIP device, HIP error during init)
+ *   2  device allocation failed
+ *   3  XTQ_VIT_DEVIDX names no device
+ *   4  HIP runtime error during a run
+ *   5  request exceeds XTQ_VIT_MAXBYTES (device bytes for X/states/scratch)
+ *   6  nseq <= 0 or nseq > XTQ_VIT_MAXSEQ
+ *   8  unsupported code (e.g. "ih2x2"; only fp16-exact V=1 codebooks run)
+ *   9  K outside 2..7 (or K != 4 for the K=4-only reference codes)
+ *  10  pivot outside [0,256) or margin < 0
+ *  11  a target is NaN
+ *  12  null pointer argument
+ *
+ * Environment:
+ *   XTQ_VIT_DEVIDX   device index for the host-pointer entries (default: the
+ *                    calling thread's current HIP device)
+ *   XTQ_VIT_MAXSEQ   upper bound on nseq per call (default 1<<24)
+ *   XTQ_VIT_MAXBYTES upper bound on library-owned device bytes (default 64 GiB)
+ *   XTQ_VIT_SCRATCH  backpointer scratch budget in bytes; larger batches are
+ *                    processed in chunks (default 8 GiB)
+ *   XTQ_VIT_GROUP    force 1, 2 or 4 sequences per forward workgroup
+ *                    (testing; default chosen from the batch size)
+ */
+#ifndef EXL3_VIT_H
+#define EXL3_VIT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * Replaces quantize/viterbi_esimd.cpp:935 xtq_vit_init (bound by
+ * quantize.py:497-503).  Selects the device (XTQ_VIT_DEVIDX) and uploads the
+ * codebook tables.  Idempotent.
+ */
+int xtq_vit_init(void);
+
+/*
+ * Replaces quantize/viterbi_esimd.cpp:970 xtq_vit_run (bound by
+ * quantize.py:499-501,604-606).  Host pointers, synchronous.
+ *   X     [nseq][256] fp32 host
+ *   code  "mul1p", "mul1" or "mul1t" (the reference's K=4 mul1 kernels; all
+ *         three give identical results); "ih2x2" returns 8
+ *   out   [nseq][256] int32 host: the pass-2 states
+ */
+int xtq_vit_run(const float* X, int nseq, const char* code, int margin, int pivot,
+                int32_t* out);
+
+/*
+ * K-aware host-pointer variant of xtq_vit_run (no reference counterpart: the
+ * reference kernel is K=4 only, viterbi_esimd.cpp:83,352; the torch path it
+ * generalises is quantize.py:323-354).  code: "mul1", "3inst" or "mcg".
+ */
+int xtq_vit_run_k(const float* X, int nseq, int K, const char* code, int margin,
+                  int pivot, int32_t* out);
+
+/*
+ * Device-pointer tail-biting encoder: the HIP counterpart of
+ * quantize_seq_tailbite (quantize.py:323-354) for torch-ROCm tensors.
+ * Stream-ordered on `stream` (a hipStream_t, 0 = default stream) and
+ * synchronous on return (the NaN check reads a device flag).
+ *   dX        [nseq][256] fp32 device
+ *   d_states  [nseq][256] int32 device, or NULL
+ *   d_trellis [nseq][16K] int16 device (EXL3 trellis slices, pack_states
+ *             layout quantize.py:360-378), or NULL
+ */
+int xtq_vit_tailbite_dev(const float* dX, int nseq, int K, const char* code,
+                         int margin, int pivot, int32_t* d_states,
+                         int16_t* d_trellis, void* stream);
+
+/*
+ * Device-pointer trellis decode: the HIP counterpart of decode_trellis
+ * (quantize.py:405-415) and of exl3xpu's reconstruct (patch 0001:60-75).
+ *   d_trellis [tk][tn][16K] int16 device
+ *   d_out_f32 [16tk][16tn] fp32 device, or NULL
+ *   d_out_f16 [16tk][16tn] fp16 (bit patterns) device, or NULL
+ */
+int xtq_trellis_decode_dev(const int16_t* d_trellis, int tk, int tn, int K,
+                           const char* code, float* d_out_f32, uint16_t* d_out_f16,
+                           void* stream);
+
+/* Device-pointer pack_states / unpack_states (quantize.py:360-402). */
+int xtq_trellis_pack_dev(const int32_t* d_states, int nt, int K, int16_t* d_trellis,
+                         void* stream);
+int xtq_trellis_unpack_dev(const int16_t* d_trellis, int nt, int K, int32_t* d_states,
+                           void* stream);
+
+/*
+ * Copies the fp32 decode table of `code` (65536 entries) into host memory
+ * (the values get_lut returns, quantize.py:90-97).
+ */
+int xtq_vit_get_lut(const char* code, float* out);
+
+/* Backpointer scratch bytes per sequence for K (sizing information). */
+int64_t xtq_vit_scratch_per_seq(int K);
+
+/* Static description of a status code. */
+const char* xtq_vit_strerror(int rc);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EXL3_VIT_H */

@@ -1,0 +1,160 @@
+#!/usr/bin/env python3
+"""make_golden.py -- write the golden fixtures in tests/golden/ from the reference.
+
+Run once, in the build container only (the reference tree is not present on
+the GPU host):
+
+    python tests/golden/make_golden.py /root/reference/quantize
+
+It imports the reference quantizer module (quantize/quantize.py) on CPU and
+records input/output vectors for the functions that closed forms, invariants
+and brute force cannot pin:
+  * quantize_seq_tailbite states on Gaussian and tie-heavy inputs, every K in
+    2..7, margins {0, 16}, pivots {0, 128, 147, 255}   (quantize.py:323-354)
+  * viterbi() free and back_from runs                   (quantize.py:218-320)
+  * pack_states / unpack_states / decode_trellis        (quantize.py:360-415)
+  * sign_vec values                                     (quantize.py:179-182)
+  * quantize_linear on a 128x128 weight, identity and AR(1) Hessians,
+    channel_scales off and on                            (quantize.py:750-875)
+  * quantize() harness with a U factor, margin 16        (quantize.py:894-966)
+  * prepare_incoherence                                  (quantize.py:969-1058)
+Only data (inputs and expected outputs) is written, as compressed .npz files
+loadable with numpy.load(allow_pickle=False).
+"""
+from __future__ import annotations
+
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+OUT = os.path.dirname(os.path.abspath(__file__))
+
+
+def ar1_hessian(d: int, n_s: int, rho: float, seed: int) -> torch.Tensor:
+    g = torch.Generator().manual_seed(seed + 100)
+    Z = torch.randn(n_s, d, generator=g, dtype=torch.float64)
+    X = torch.empty_like(Z)
+    X[:, 0] = Z[:, 0]
+    c = (1.0 - rho * rho) ** 0.5
+    for i in range(1, d):
+        X[:, i] = rho * X[:, i - 1] + c * Z[:, i]
+    return (X.t() @ X / n_s).float()
+
+
+def tie_heavy_inputs(lut: np.ndarray, rng: np.random.Generator, n: int):
+    """Targets that force exact cost ties: exact LUT values, zeros, a coarse grid."""
+    X = np.empty((n, 256), dtype=np.float32)
+    for q in range(n):
+        kind = q % 3
+        if kind == 0:
+            X[q] = lut[rng.integers(0, lut.size, 256)]
+        elif kind == 1:
+            X[q] = 0.0
+            X[q, rng.integers(0, 256, 16)] = lut[rng.integers(0, lut.size, 16)]
+        else:
+            X[q] = np.round(rng.standard_normal(256) * 2.0) / 2.0
+    return X
+
+
+def main(refdir: str):
+    sys.path.insert(0, refdir)
+    import quantize as xq  # the reference module, CPU only
+    torch.set_num_threads(8)
+    lut = xq.get_lut("exl3_mul1", 16)
+    lut_np = lut.numpy().astype(np.float32)
+    np.savez_compressed(os.path.join(OUT, "lut_mul1.npz"), lut=lut_np,
+                        perm=xq.tensor_core_perm().numpy().astype(np.int32))
+
+    # ---------------------------------------------------- tail-bite states
+    t0 = time.time()
+    rng = np.random.default_rng(20261011)
+    pivots = (0, 128, 147, 255)
+    margins = (0, 16)
+    data = {}
+    for K in range(2, 8):
+        g = rng.standard_normal((3, 256)).astype(np.float32)
+        ties = tie_heavy_inputs(lut_np, rng, 3)
+        X = np.concatenate([g, ties], 0)                 # [6, 256]
+        data[f"X_K{K}"] = X
+        Xt = torch.from_numpy(X.T.copy())                # [256, 6]
+        for m in margins:
+            for p in pivots:
+                st = xq.quantize_seq_tailbite(Xt, lut, K, 16, pivot=p, margin=m)
+                data[f"S_K{K}_m{m}_p{p}"] = st.t().numpy().astype(np.int32)
+        # plain viterbi: free, and back_from on a truncated run
+        st = xq.viterbi(Xt, lut, K, 16)
+        data[f"V_K{K}"] = st.t().numpy().astype(np.int32)
+        sb = xq.viterbi(Xt[:150], lut, K, 16, back_from=100)
+        data[f"VB_K{K}"] = sb.numpy().astype(np.int32)
+        ov = torch.from_numpy((np.arange(6) * 977) % (1 << (16 - K)))
+        sp = xq.viterbi(Xt, lut, K, 16, overlap=ov)
+        data[f"VP_K{K}"] = sp.t().numpy().astype(np.int32)
+        data[f"VPov_K{K}"] = ov.numpy().astype(np.int32)
+        # pack / unpack / decode of the pass-2 states (pivot 128, margin 0)
+        s128 = torch.from_numpy(data[f"S_K{K}_m0_p128"].astype(np.int64))
+        packed = xq.pack_states(s128, K)
+        data[f"P_K{K}"] = packed.numpy()
+        data[f"U_K{K}"] = xq.unpack_states(packed, K).numpy().astype(np.int32)
+        tr = packed.view(2, 3, 16 * K)
+        data[f"D_K{K}"] = xq.decode_trellis(tr, lut, K, 32, 48).numpy()
+        print(f"  K={K} done {time.time() - t0:.1f}s", flush=True)
+    np.savez_compressed(os.path.join(OUT, "tailbite.npz"), **data)
+
+    # ----------------------------------------------------------- sign vectors
+    sv = {f"sign_{n}_{s}": xq.sign_vec(n, s).numpy().astype(np.float32)
+          for n in (128, 256) for s in (20261011, 20261012, 7)}
+    np.savez_compressed(os.path.join(OUT, "sign_vec.npz"), **sv)
+
+    # ------------------------------------------------- end-to-end, 128 x 128
+    e2e = {}
+    g0 = torch.Generator().manual_seed(0)
+    W = torch.randn(128, 128, generator=g0).half().float()
+    H_ar = ar1_hessian(128, 512, 0.5, 0)
+    e2e["W"] = W.numpy()
+    e2e["H_ar"] = H_ar.numpy()
+    cases = (("id", torch.eye(128), False, True),
+             ("ar", H_ar, False, True),
+             ("arcs", H_ar, True, True),
+             ("nold", H_ar, False, False))
+    for tag, H, cs, ldlq in cases:
+        r = xq.quantize_linear(W, H, code="exl3_mul1", K=4, use_ldlq=ldlq,
+                               margin=0, channel_scales=cs)
+        e2e[f"{tag}_W_hat"] = r["W_hat"].numpy()
+        e2e[f"{tag}_trellis"] = r["trellis"].numpy()
+        e2e[f"{tag}_suh"] = r["suh"].float().numpy()
+        e2e[f"{tag}_svh"] = r["svh"].float().numpy()
+        e2e[f"{tag}_Wscale"] = np.float32(r["Wscale"])
+        e2e[f"{tag}_herr"] = np.float64(xq.hessian_weighted_err(W, r["W_hat"], H))
+        e2e[f"{tag}_relmse"] = np.float64(xq.rel_mse(W, r["W_hat"]))
+        print(f"  quantize_linear {tag} done {time.time() - t0:.1f}s", flush=True)
+
+    # quantize() harness: inner-domain weight + U factor (U^T U = G^-1)
+    prep = xq.prepare_incoherence(W, H_ar, channel_scales=True)
+    e2e["prep_Wt"] = prep["Wt"].numpy()
+    e2e["prep_G"] = prep["G"].numpy()
+    e2e["prep_suh"] = prep["suh"].numpy()
+    e2e["prep_svh"] = prep["svh"].numpy()
+    G = prep["G"].clone()
+    G.diagonal().add_(0.01 * G.diagonal().mean())
+    Gi = torch.cholesky_inverse(torch.linalg.cholesky(G.double()))
+    U = torch.linalg.cholesky(Gi, upper=True).float()
+    e2e["q_U"] = U.numpy()
+    Wh, packed, scale = xq.quantize(prep["Wt"], U, "exl3_mul1", 4, seed=147,
+                                    margin=16)
+    e2e["q_W_hat"] = Wh.numpy()
+    e2e["q_packed"] = packed.numpy()
+    e2e["q_scale"] = np.float32(scale)
+    Wh0, packed0, scale0 = xq.quantize(prep["Wt"][:64], None, "exl3_mul1", 3,
+                                       seed=5, margin=0)
+    e2e["q0_W_hat"] = Wh0.numpy()
+    e2e["q0_packed"] = packed0.numpy()
+    e2e["q0_scale"] = np.float32(scale0)
+    np.savez_compressed(os.path.join(OUT, "e2e_128.npz"), **e2e)
+    print(f"done {time.time() - t0:.1f}s")
+
+
+if __name__ == "__main__":
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference/quantize")

@@ -1,0 +1,160 @@
+"""GPU parity of the HIP tail-biting encoder, decode and pack kernels.
+
+Every check compares libexl3vit.so (called through its C-ABI via ctypes)
+with the reference's golden vectors or the CPU oracle on identical inputs,
+bit for bit.  Reference semantics: quantize.py:218-415.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import load_golden
+
+pytestmark = pytest.mark.gpu
+
+PIVOTS = (0, 128, 147, 255)
+MARGINS = (0, 16)
+
+
+@pytest.fixture(scope="module")
+def hb():
+    import hip_backend
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    hip_backend.lib()
+    return hip_backend
+
+
+def _run(hb, X: np.ndarray, K: int, pivot: int, margin: int, trellis=False):
+    Xd = torch.from_numpy(np.ascontiguousarray(X, dtype=np.float32)).cuda()
+    st, tr = hb.tailbite(Xd, K, pivot, margin, states=True, trellis=trellis)
+    torch.cuda.synchronize()
+    return st.cpu().numpy(), (tr.cpu().numpy() if tr is not None else None)
+
+
+@pytest.mark.parametrize("K", range(2, 8))
+def test_golden_tailbite(hb, K):
+    """States equal the reference's own quantize_seq_tailbite on Gaussian and
+    tie-heavy targets for every margin/pivot in the fixture."""
+    g = load_golden("tailbite.npz")
+    X = g[f"X_K{K}"]
+    for m in MARGINS:
+        for p in PIVOTS:
+            print(f"case K={K} margin={m} pivot={p}", flush=True)
+            st, tr = _run(hb, X, K, p, m, trellis=(m == 0 and p == 128))
+            np.testing.assert_array_equal(st, g[f"S_K{K}_m{m}_p{p}"],
+                                          err_msg=f"K={K} m={m} p={p}")
+            if tr is not None:
+                np.testing.assert_array_equal(tr, g[f"P_K{K}"])
+
+
+@pytest.mark.parametrize("K", range(2, 8))
+@pytest.mark.parametrize("group", ["1", "2", "4"])
+def test_oracle_random(hb, oracle_mod, mul1_lut, K, group, monkeypatch):
+    """Random Gaussian and tie-heavy batches against the oracle, with each
+    sequences-per-workgroup code path forced, odd batch sizes included."""
+    monkeypatch.setenv("XTQ_VIT_GROUP", group)
+    rng = np.random.default_rng(1000 * K + int(group))
+    n = 7
+    X = rng.standard_normal((n, 256)).astype(np.float32)
+    X[1] = mul1_lut[rng.integers(0, 65536, 256)]          # exact codebook values
+    X[2] = 0.0                                             # all ties at step 0
+    X[3] *= 40.0                                           # large costs
+    X[4] = np.round(X[4] * 2) / 2                          # coarse grid
+    for pivot, margin in ((128, 0), (3, 16), (250, 16), (200, 100)):
+        print(f"case K={K} group={group} pivot={pivot} margin={margin}", flush=True)
+        want = oracle_mod.tailbite(X, mul1_lut, K, 16, pivot=pivot, margin=margin)
+        got, tr = _run(hb, X, K, pivot, margin, trellis=True)
+        np.testing.assert_array_equal(got, want)
+        np.testing.assert_array_equal(tr, oracle_mod.pack(want, K))
+
+
+@pytest.mark.parametrize("K", (2, 4, 7))
+def test_batch_position_invariance(hb, K):
+    """A sequence encodes identically wherever it sits in a large batch
+    (chunking and grouping never mix sequences)."""
+    rng = np.random.default_rng(7 + K)
+    n = 2100
+    X = rng.standard_normal((n, 256)).astype(np.float32)
+    print(f"case K={K} n={n}", flush=True)
+    st_all, _ = _run(hb, X, K, 147, 16)
+    idx = np.array([0, 1, 2, 511, 1024, 1500, 2098, 2099])
+    st_few, _ = _run(hb, X[idx], K, 147, 16)
+    np.testing.assert_array_equal(st_all[idx], st_few)
+    # tail-bite wrap invariant on the whole batch (verify_viterbi.py:61-64)
+    SP = 1 << (16 - K)
+    assert ((st_all[:, 0] >> K) == (st_all[:, -1] & (SP - 1))).all()
+
+
+@pytest.mark.parametrize("K", range(2, 8))
+def test_decode_unpack_pack(hb, oracle_mod, mul1_lut, K):
+    """decode/unpack/pack kernels equal the oracle and the reference fixture."""
+    g = load_golden("tailbite.npz")
+    P = g[f"P_K{K}"]                                       # [6, 16K] from the reference
+    tr = torch.from_numpy(P).cuda().view(2, 3, 16 * K)
+    w = hb.decode(tr, K)
+    np.testing.assert_array_equal(w.cpu().numpy(), g[f"D_K{K}"])
+    w16 = hb.decode(tr, K, dtype=torch.float16)
+    np.testing.assert_array_equal(w16.float().cpu().numpy(), g[f"D_K{K}"])
+    st = hb.unpack(tr.view(-1, 16 * K), K)
+    np.testing.assert_array_equal(st.cpu().numpy(), g[f"U_K{K}"])
+    rp = hb.pack(st, K)
+    np.testing.assert_array_equal(rp.cpu().numpy(), P)
+    rng = np.random.default_rng(K)
+    rnd = rng.integers(-32768, 32768, (5, 7, 16 * K)).astype(np.int16)
+    w = hb.decode(torch.from_numpy(rnd).cuda(), K)
+    np.testing.assert_array_equal(w.cpu().numpy(), oracle_mod.decode(rnd, mul1_lut, K))
+
+
+def test_nan_target_rejected(hb):
+    X = torch.randn(3, 256, device="cuda")
+    X[1, 17] = float("nan")
+    with pytest.raises(hb.HipViterbiError) as ei:
+        hb.tailbite(X, 4, 128, 0)
+    assert ei.value.rc == 11
+    # the library recovers: a clean call afterwards succeeds
+    st, _ = hb.tailbite(torch.randn(2, 256, device="cuda"), 4, 128, 0)
+    assert st.shape == (2, 256)
+
+
+def test_inf_targets_match_oracle(hb, oracle_mod, mul1_lut):
+    """+-inf targets give all-inf costs; ties resolve like the reference."""
+    X = np.random.default_rng(3).standard_normal((2, 256)).astype(np.float32)
+    X[0, 5] = np.inf
+    X[1, 100:110] = -np.inf
+    want = oracle_mod.tailbite(X, mul1_lut, 4, 16, pivot=128, margin=0)
+    got, _ = _run(hb, X, 4, 128, 0)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_host_entry_matches_device(hb, mul1_lut):
+    """xtq_vit_run (reference ABI, host pointers, K=4) equals the device entry."""
+    import ctypes
+    X = np.random.default_rng(11).standard_normal((5, 256)).astype(np.float32)
+    out = np.empty((5, 256), dtype=np.int32)
+    rc = hb.lib().xtq_vit_run(X.ctypes.data_as(ctypes.c_void_p), 5, b"mul1p", 16, 147,
+                              out.ctypes.data_as(ctypes.c_void_p))
+    assert rc == 0
+    got, _ = _run(hb, X, 4, 147, 16)
+    np.testing.assert_array_equal(out, got)
+    out2 = np.empty((5, 256), dtype=np.int32)
+    rc = hb.lib().xtq_vit_run_k(X.ctypes.data_as(ctypes.c_void_p), 5, 6, b"mul1", 0, 9,
+                                out2.ctypes.data_as(ctypes.c_void_p))
+    assert rc == 0
+    got6, _ = _run(hb, X, 6, 9, 0)
+    np.testing.assert_array_equal(out2, got6)
+    rc = hb.lib().xtq_vit_run(X.ctypes.data_as(ctypes.c_void_p), 5, b"ih2x2", 0, 128,
+                              out.ctypes.data_as(ctypes.c_void_p))
+    assert rc == 8
+
+
+def test_other_codebooks(hb, oracle_mod):
+    """3inst and mcg codebooks (fp16-exact) run through the same kernel."""
+    X = np.random.default_rng(5).standard_normal((3, 256)).astype(np.float32)
+    for name, short in (("exl3_3inst", "3inst"), ("exl3_mcg", "mcg")):
+        lut = oracle_mod.code_lut(name)
+        want = oracle_mod.tailbite(X, lut, 3, 16, pivot=128, margin=0)
+        Xd = torch.from_numpy(X).cuda()
+        st, _ = hb.tailbite(Xd, 3, 128, 0, code=short)
+        np.testing.assert_array_equal(st.cpu().numpy(), want)
