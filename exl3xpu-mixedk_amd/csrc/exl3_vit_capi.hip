@@ -198,10 +198,8 @@ int chunk_size(const DevCtx& cx, int K, int nseq) {
     return (int)ch;
 }
 
-// The two-pass tail-biting schedule over device buffers (quantize.py:323-354).
-int run_tailbite(DevCtx& cx, const float* dX, int nseq, int K, Code code, int margin,
-                 int pivot, int32_t* d_states, int16_t* d_trellis, hipStream_t s) {
-    const int chunk = chunk_size(cx, K, nseq);
+// Grows the backpointer/final-state scratch for `chunk` sequences of K.
+int reserve_scratch(DevCtx& cx, int K, int chunk) {
     const size_t per = xtq::bp_tile_bytes(K);
     // Device bytes this call adds to what the library already holds.
     size_t add = 0;
@@ -221,38 +219,11 @@ int run_tailbite(DevCtx& cx, const float* dX, int nseq, int K, Code code, int ma
         if (grow(&cx.ov, &sc2, (size_t)chunk, sizeof(int32_t), &cx.owned)) return 2;
         cx.seq_cap = sc;
     }
-    const int n1 = (margin > 0 && pivot + margin < xtq::kSteps) ? pivot + margin : xtq::kSteps;
-    const uint16_t* lut = cx.lut16[code];
-    for (int c0 = 0; c0 < nseq; c0 += chunk) {
-        const int n = (nseq - c0) < chunk ? (nseq - c0) : chunk;
-        const float* x = dX + (size_t)c0 * xtq::kSteps;
-        int T = xtq::forward_group(K, n, cx.ncu);
-        if (const char* g = getenv("XTQ_VIT_GROUP")) {
-            // Test hook: force the sequences-per-workgroup (1, 2 or 4),
-            // clamped to what the LDS footprint for K allows.
-            const int want = atoi(g);
-            const int cap = xtq::forward_group(K, 1 << 30, 1);
-            if (want == 1 || want == 2 || want == 4) T = want < cap ? want : cap;
-        }
-        hipError_t e;
-        e = xtq::launch_forward(K, x, n, lut, 1, pivot, n1, pivot, nullptr, cx.bp, cx.send,
-                                cx.err, T, s);
-        if (e == hipSuccess)
-            e = xtq::launch_traceback(K, cx.bp, n, cx.send, 1, pivot, n1, cx.ov, nullptr,
-                                      nullptr, s);
-        if (e == hipSuccess)
-            e = xtq::launch_forward(K, x, n, lut, 2, 0, xtq::kSteps, 0, cx.ov, cx.bp, cx.send,
-                                    cx.err, T, s);
-        if (e == hipSuccess)
-            e = xtq::launch_traceback(
-                K, cx.bp, n, cx.send, 2, 0, xtq::kSteps, nullptr,
-                d_states ? d_states + (size_t)c0 * xtq::kSteps : nullptr,
-                d_trellis ? d_trellis + (size_t)c0 * 16 * K : nullptr, s);
-        if (e != hipSuccess) {
-            fprintf(stderr, "xtq_vit run: %s\n", hipGetErrorString(e));
-            return 4;
-        }
-    }
+    return 0;
+}
+
+// Waits for the stream and turns the device NaN flag into status 11.
+int finish(DevCtx& cx, hipStream_t s) {
     uint32_t herr = 0;
     if (hipMemcpyAsync(&herr, cx.err, sizeof(herr), hipMemcpyDeviceToHost, s) != hipSuccess ||
         hipStreamSynchronize(s) != hipSuccess) {
@@ -265,6 +236,86 @@ int run_tailbite(DevCtx& cx, const float* dX, int nseq, int K, Code code, int ma
         return 11;
     }
     return 0;
+}
+
+int pick_group(const DevCtx& cx, int K, int n) {
+    int T = xtq::forward_group(K, n, cx.ncu);
+    if (const char* g = getenv("XTQ_VIT_GROUP")) {
+        // Test hook: force the sequences per workgroup (1, 2 or 4), clamped
+        // to what the LDS footprint for K allows.
+        const int want = atoi(g);
+        const int cap = xtq::forward_group(K, 1 << 30, 1);
+        if (want == 1 || want == 2 || want == 4) T = want < cap ? want : cap;
+    }
+    return T;
+}
+
+// The two-pass tail-biting schedule over device buffers (quantize.py:323-354).
+int run_tailbite(DevCtx& cx, const float* dX, int nseq, int K, Code code, int margin,
+                 int pivot, int32_t* d_states, int16_t* d_trellis, hipStream_t s) {
+    const int chunk = chunk_size(cx, K, nseq);
+    int rc = reserve_scratch(cx, K, chunk);
+    if (rc) return rc;
+    const int n1 = (margin > 0 && pivot + margin < xtq::kSteps) ? pivot + margin : xtq::kSteps;
+    const uint16_t* lut = cx.lut16[code];
+    for (int c0 = 0; c0 < nseq; c0 += chunk) {
+        const int n = (nseq - c0) < chunk ? (nseq - c0) : chunk;
+        const float* x = dX + (size_t)c0 * xtq::kSteps;
+        const int T = pick_group(cx, K, n);
+        hipError_t e;
+        // Pass 1: free run over the sequence rolled right by pivot, n1 steps,
+        // traced back to step pivot: ov = s_pivot >> K.
+        e = xtq::launch_forward(K, x, xtq::kSteps, xtq::kSteps, n, lut, pivot, n1, pivot,
+                                nullptr, cx.bp, cx.send, cx.err, T, s);
+        if (e == hipSuccess)
+            e = xtq::launch_traceback(K, cx.bp, n, cx.send, n1, pivot, K, cx.ov, nullptr,
+                                      nullptr, s);
+        // Pass 2: run pinned to ov on the unrolled sequence, full traceback.
+        if (e == hipSuccess)
+            e = xtq::launch_forward(K, x, xtq::kSteps, xtq::kSteps, n, lut, 0, xtq::kSteps, 0,
+                                    cx.ov, cx.bp, cx.send, cx.err, T, s);
+        if (e == hipSuccess)
+            e = xtq::launch_traceback(
+                K, cx.bp, n, cx.send, xtq::kSteps, 0, 0, nullptr,
+                d_states ? d_states + (size_t)c0 * xtq::kSteps : nullptr,
+                d_trellis ? d_trellis + (size_t)c0 * 16 * K : nullptr, s);
+        if (e != hipSuccess) {
+            fprintf(stderr, "xtq_vit run: %s\n", hipGetErrorString(e));
+            return 4;
+        }
+    }
+    return finish(cx, s);
+}
+
+// One Viterbi run (quantize.py:218-320) over device buffers: free or pinned,
+// full traceback or only the state at back_from.
+int run_viterbi(DevCtx& cx, const float* dX, int nseq, int T, int K, Code code,
+                const int32_t* d_ov, int back_from, int32_t* d_out, hipStream_t s) {
+    const int chunk = chunk_size(cx, K, nseq);
+    int rc = reserve_scratch(cx, K, chunk);
+    if (rc) return rc;
+    const uint16_t* lut = cx.lut16[code];
+    const int stop = back_from >= 0 ? back_from : 0;
+    for (int c0 = 0; c0 < nseq; c0 += chunk) {
+        const int n = (nseq - c0) < chunk ? (nseq - c0) : chunk;
+        const int G = pick_group(cx, K, n);
+        hipError_t e = xtq::launch_forward(K, dX + (size_t)c0 * T, T, T, n, lut, 0, T, stop,
+                                           d_ov ? d_ov + c0 : nullptr, cx.bp, cx.send,
+                                           cx.err, G, s);
+        if (e == hipSuccess) {
+            if (back_from >= 0)
+                e = xtq::launch_traceback(K, cx.bp, n, cx.send, T, back_from, 0, d_out + c0,
+                                          nullptr, nullptr, s);
+            else
+                e = xtq::launch_traceback(K, cx.bp, n, cx.send, T, 0, 0, nullptr,
+                                          d_out + (size_t)c0 * T, nullptr, s);
+        }
+        if (e != hipSuccess) {
+            fprintf(stderr, "xtq_vit viterbi: %s\n", hipGetErrorString(e));
+            return 4;
+        }
+    }
+    return finish(cx, s);
 }
 
 // Host-pointer tail-bite: stage X, run, copy the states back.
@@ -375,6 +426,26 @@ int xtq_vit_tailbite_dev(const float* dX, int nseq, int K, const char* code, int
     if (rc) return rc;
     return run_tailbite(g_dev[dev], dX, nseq, K, c, margin, pivot, d_states, d_trellis,
                         (hipStream_t)stream);
+}
+
+int xtq_vit_viterbi_dev(const float* dX, int nseq, int T, int K, const char* code,
+                        const int32_t* d_overlap, int back_from, int32_t* d_out,
+                        void* stream) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!dX || !d_out) return 12;
+    Code c;
+    int rc = parse_code(code, &c);
+    if (rc) return rc;
+    read_env();
+    if (nseq <= 0 || nseq > g_maxseq) return 6;
+    if (K < 2 || K > 7) return 9;
+    if (T < 1 || T > xtq::kSteps || back_from < -1 || back_from >= T) return 10;
+    int dev = 0;
+    if (current_device(&dev)) return 1;
+    rc = dev_init(dev);
+    if (rc) return rc;
+    return run_viterbi(g_dev[dev], dX, nseq, T, K, c, d_overlap, back_from, d_out,
+                       (hipStream_t)stream);
 }
 
 int xtq_trellis_decode_dev(const int16_t* d_trellis, int tk, int tn, int K, const char* code,

@@ -28,26 +28,30 @@ inline size_t bp_tile_bytes(int K) { return (size_t)kSlots * bp_step_bytes(K); }
 // device with ncu compute units (LDS bounds it by K; small launches use 1).
 int forward_group(int K, int nseq, int ncu);
 
-// Forward DP of one pass for nseq sequences.
-//   X       [nseq][256] fp32 targets (device)
+// Forward DP of one Viterbi run for nseq sequences.
+//   X, xstride, xlen  targets: row q holds xlen fp32 values at X + q*xstride
 //   lut16   [65536] fp16 bit patterns of the codebook (device)
-//   pass    1: free start, rolled by pivot, nsteps = n1;  2: pinned to ov_in
-//   store_lo first step index whose backpointers are kept
+//   roll    step i reads target (i - roll) mod xlen (roll != 0 needs xlen 256)
+//   nsteps  steps of the run (<= xlen when roll == 0)
+//   store_lo first step whose backpointers are kept (steps store_lo..nsteps-2)
+//   ov_in   [nseq] pin values, or NULL for a free run; a pinned run pins
+//           s_0 >> K == ov and s_last mod 2^(16-K) == ov (quantize.py:265-303)
 //   bp      backpointer scratch, bp_tile_bytes(K) per sequence (device)
-//   send    [nseq] final state of the pass (device, out)
+//   send    [nseq] final state of the run (device, out)
 //   err     device word, OR-ed with 1 when a target is NaN
-hipError_t launch_forward(int K, const float* X, int nseq, const uint16_t* lut16,
-                          int pass, int pivot, int nsteps, int store_lo,
-                          const int32_t* ov_in, void* bp, int32_t* send,
-                          uint32_t* err, int group, hipStream_t stream);
+hipError_t launch_forward(int K, const float* X, int xstride, int xlen, int nseq,
+                          const uint16_t* lut16, int roll, int nsteps, int store_lo,
+                          const int32_t* ov_in, void* bp, int32_t* send, uint32_t* err,
+                          int group, hipStream_t stream);
 
-// Traceback of one pass.  Pass 1 writes ov_out[q] = s_pivot >> K.  Pass 2
-// writes the 256 states (states, nullable) and/or the packed EXL3 trellis
-// (trellis [nseq][16K] int16, nullable).
+// Traceback of one run from send (the state at step nsteps-1) down to step
+// `stop`.  Writes sout[q] = s_stop >> shift (nullable), the nsteps states
+// (states [nseq][nsteps], nullable; needs stop == 0) and/or the packed EXL3
+// trellis (trellis [nseq][16K] int16, nullable; needs stop == 0 and
+// nsteps == 256).
 hipError_t launch_traceback(int K, const void* bp, int nseq, const int32_t* send,
-                            int pass, int pivot, int nsteps, int32_t* ov_out,
-                            int32_t* states, int16_t* trellis,
-                            hipStream_t stream);
+                            int nsteps, int stop, int shift, int32_t* sout,
+                            int32_t* states, int16_t* trellis, hipStream_t stream);
 
 // Trellis decode: int16 [tk][tn][16K] -> [16tk][16tn] (fp32 or fp16 bits).
 hipError_t launch_decode(int K, const int16_t* trellis, int tk, int tn,

@@ -106,8 +106,9 @@ __device__ __forceinline__ int bp_lookup(const uint8_t* row, int j) {
 // codebook registers are shared by the T sequences; one barrier per step).
 template <int K, int T>
 __global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
-    const float* __restrict__ X, int nseq, const uint16_t* __restrict__ lut16, int pass,
-    int pivot, int nsteps, int store_lo, const int32_t* __restrict__ ov_in,
+    const float* __restrict__ X, int xstride, int xlen, int nseq,
+    const uint16_t* __restrict__ lut16, int roll, int nsteps, int store_lo,
+    const int32_t* __restrict__ ov_in,
     uint8_t* __restrict__ bp, int32_t* __restrict__ send, uint32_t* __restrict__ err,
     float one) {
     using G = Geom<K>;
@@ -122,13 +123,15 @@ __global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
     if (tid < T * kSteps) {
         const int tt = tid / kSteps, e = tid % kSteps;
         float v = 0.0f;
-        if (tt < ntile) {
-            v = X[(size_t)(q0 + tt) * kSteps + e];
+        if (tt < ntile && e < xlen) {
+            v = X[(size_t)(q0 + tt) * xstride + e];
             if (v != v) atomicOr(err, 1u);
         }
         xs[tt][e] = v;
     }
-    if (tid < T) ovs[tid] = (pass == 2 && tid < ntile) ? ov_in[q0 + tid] : -1;
+    // Pinned runs (ov_in given) pin both ends to their ov; free runs use -1.
+    const bool pinned = (ov_in != nullptr);
+    if (tid < T) ovs[tid] = (pinned && tid < ntile) ? ov_in[q0 + tid] : -1;
 
     // Owned groups and candidates: groups j_c = jbase + c, candidate w of a
     // group is state j_c + (wbase + w) * SP; local index l = c*W + w.
@@ -167,7 +170,8 @@ __global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
 
     const int a0 = jbase >> K;  // first NC x NC block this thread reads
     for (int i = 0; i < nsteps; ++i) {
-        const int u = (pass == 1) ? ((i - pivot) & (kSteps - 1)) : i;
+        // Target of step i of the sequence rolled right by `roll`.
+        const int u = (i - roll < 0) ? i - roll + xlen : i - roll;
 #pragma unroll 1
         for (int tt = 0; tt < ntile; ++tt) {
             // Keep the fp16 codebook pairs opaque per sequence-step so the
@@ -249,7 +253,7 @@ __global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
                             (unit_t)bits;
                     }
                 }
-            } else if (pass == 2) {
+            } else if (pinned) {
                 // Pinned end: the allowed final states are exactly group ov's
                 // candidates, so s_end = ov + argmin_w * SP.  When even the
                 // best allowed cost is +inf, cost + mask is +inf everywhere
@@ -296,9 +300,9 @@ __global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
 // ---------------------------------------------------------------- traceback
 template <int K>
 __global__ __launch_bounds__(kTbThreads) void tb_kernel(
-    const uint8_t* __restrict__ bp, const int32_t* __restrict__ send, int pass,
-    int pivot, int nsteps, int32_t* __restrict__ ov_out,
-    int32_t* __restrict__ states, int16_t* __restrict__ trellis) {
+    const uint8_t* __restrict__ bp, const int32_t* __restrict__ send, int nsteps, int stop,
+    int shift, int32_t* __restrict__ sout, int32_t* __restrict__ states,
+    int16_t* __restrict__ trellis) {
     using G = Geom<K>;
     constexpr int STAGE = 32768;
     constexpr int CH = STAGE / G::BPSTEP;  // slots per staged chunk
@@ -308,10 +312,10 @@ __global__ __launch_bounds__(kTbThreads) void tb_kernel(
 
     const int q = blockIdx.x, tid = threadIdx.x;
     const uint8_t* bpq = bp + (size_t)q * ((size_t)kSlots * G::BPSTEP);
-    const int stop = (pass == 1) ? pivot : 0;
+    const bool keep = (states != nullptr) || (trellis != nullptr);
     if (tid == 0) {
         cur = send[q] & 0xFFFF;
-        if (pass == 2) st[nsteps - 1] = cur;
+        if (keep) st[nsteps - 1] = cur;
     }
     // Step i (s_i -> s_{i-1}) reads slot i-1; slots stop .. nsteps-2.
     for (int hi = nsteps - 2; hi >= stop; ) {
@@ -327,21 +331,18 @@ __global__ __launch_bounds__(kTbThreads) void tb_kernel(
                 const int j = (s >> K) & (G::SP - 1);
                 const uint8_t* row = (const uint8_t*)stage + (size_t)(sl - lo) * G::BPSTEP;
                 s = j + bp_lookup<K>(row, j) * G::SP;
-                if (pass == 2) st[sl] = s;
+                if (keep) st[sl] = s;
             }
             cur = s;
         }
         hi = lo - 1;
     }
     __syncthreads();
-    if (pass == 1) {
-        if (tid == 0) ov_out[q] = cur >> K;
-        return;
-    }
+    if (sout && tid == 0) sout[q] = cur >> shift;
     if (states) {
-        for (int t = tid; t < kSteps; t += kTbThreads) states[(size_t)q * kSteps + t] = st[t];
+        for (int t = tid; t < nsteps; t += kTbThreads) states[(size_t)q * nsteps + t] = st[t];
     }
-    if (trellis) {
+    if (trellis && nsteps == kSteps) {
         // Symbol t = s_t mod 2^K at stream bits [tK, (t+1)K), MSB first;
         // 32-bit words MSB first, stored as int16 halves, low half first.
         for (int wd = tid; wd < 8 * K; wd += kTbThreads) {
@@ -452,25 +453,27 @@ constexpr int max_group() {
 
 template <int K>
 struct FwdL {
-    static hipError_t run(const float* X, int nseq, const uint16_t* lut16, int pass,
-                          int pivot, int nsteps, int store_lo, const int32_t* ov_in,
-                          void* bp, int32_t* send, uint32_t* err, int group,
-                          hipStream_t s) {
+    static hipError_t run(const float* X, int xstride, int xlen, int nseq,
+                          const uint16_t* lut16, int roll, int nsteps, int store_lo,
+                          const int32_t* ov_in, void* bp, int32_t* send, uint32_t* err,
+                          int group, hipStream_t s) {
         const int T = group <= 1 ? 1 : group <= 2 ? 2 : 4;
         if (T > max_group<K>()) return hipErrorInvalidValue;
         const int nwg = (nseq + T - 1) / T;
         if (T == 1)
             hipLaunchKernelGGL((fwd_kernel<K, 1>), dim3(nwg), dim3(kFwdThreads), 0, s, X,
-                               nseq, lut16, pass, pivot, nsteps, store_lo, ov_in,
+                               xstride, xlen, nseq, lut16, roll, nsteps, store_lo, ov_in,
                                (uint8_t*)bp, send, err, 1.0f);
         else if constexpr (max_group<K>() >= 2) {
             if (T == 2)
                 hipLaunchKernelGGL((fwd_kernel<K, 2>), dim3(nwg), dim3(kFwdThreads), 0, s,
-                                   X, nseq, lut16, pass, pivot, nsteps, store_lo, ov_in,
+                                   X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo,
+                                   ov_in,
                                    (uint8_t*)bp, send, err, 1.0f);
             else if constexpr (max_group<K>() >= 4)
                 hipLaunchKernelGGL((fwd_kernel<K, 4>), dim3(nwg), dim3(kFwdThreads), 0, s,
-                                   X, nseq, lut16, pass, pivot, nsteps, store_lo, ov_in,
+                                   X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo,
+                                   ov_in,
                                    (uint8_t*)bp, send, err, 1.0f);
         }
         return hipGetLastError();
@@ -491,11 +494,11 @@ struct GroupSel {
 
 template <int K>
 struct TbL {
-    static hipError_t run(const void* bp, int nseq, const int32_t* send, int pass,
-                          int pivot, int nsteps, int32_t* ov_out, int32_t* states,
+    static hipError_t run(const void* bp, int nseq, const int32_t* send, int nsteps,
+                          int stop, int shift, int32_t* sout, int32_t* states,
                           int16_t* trellis, hipStream_t s) {
         hipLaunchKernelGGL(tb_kernel<K>, dim3(nseq), dim3(kTbThreads), 0, s,
-                           (const uint8_t*)bp, send, pass, pivot, nsteps, ov_out, states,
+                           (const uint8_t*)bp, send, nsteps, stop, shift, sout, states,
                            trellis);
         return hipGetLastError();
     }
@@ -549,20 +552,25 @@ int forward_group(int K, int nseq, int ncu) {
     return T;
 }
 
-hipError_t launch_forward(int K, const float* X, int nseq, const uint16_t* lut16, int pass,
-                          int pivot, int nsteps, int store_lo, const int32_t* ov_in,
-                          void* bp, int32_t* send, uint32_t* err, int group,
-                          hipStream_t stream) {
+hipError_t launch_forward(int K, const float* X, int xstride, int xlen, int nseq,
+                          const uint16_t* lut16, int roll, int nsteps, int store_lo,
+                          const int32_t* ov_in, void* bp, int32_t* send, uint32_t* err,
+                          int group, hipStream_t stream) {
     if (nseq <= 0) return hipSuccess;
-    return dispatch_k<FwdL>(K, X, nseq, lut16, pass, pivot, nsteps, store_lo, ov_in, bp,
-                            send, err, group, stream);
+    if (xlen < 1 || xlen > kSteps || nsteps < 1 || nsteps > kSteps || roll < 0 ||
+        roll >= xlen || (roll != 0 && xlen != kSteps) || (roll == 0 && nsteps > xlen))
+        return hipErrorInvalidValue;
+    return dispatch_k<FwdL>(K, X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo, ov_in,
+                            bp, send, err, group, stream);
 }
 
-hipError_t launch_traceback(int K, const void* bp, int nseq, const int32_t* send, int pass,
-                            int pivot, int nsteps, int32_t* ov_out, int32_t* states,
+hipError_t launch_traceback(int K, const void* bp, int nseq, const int32_t* send,
+                            int nsteps, int stop, int shift, int32_t* sout, int32_t* states,
                             int16_t* trellis, hipStream_t stream) {
     if (nseq <= 0) return hipSuccess;
-    return dispatch_k<TbL>(K, bp, nseq, send, pass, pivot, nsteps, ov_out, states, trellis,
+    if (nsteps < 1 || nsteps > kSteps || stop < 0 || stop >= nsteps)
+        return hipErrorInvalidValue;
+    return dispatch_k<TbL>(K, bp, nseq, send, nsteps, stop, shift, sout, states, trellis,
                            stream);
 }
 

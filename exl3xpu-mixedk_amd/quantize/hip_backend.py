@@ -50,6 +50,7 @@ def lib():
         L.xtq_vit_run.argtypes = [vp, i32, cp, i32, i32, vp]
         L.xtq_vit_run_k.argtypes = [vp, i32, i32, cp, i32, i32, vp]
         L.xtq_vit_tailbite_dev.argtypes = [vp, i32, i32, cp, i32, i32, vp, vp, vp]
+        L.xtq_vit_viterbi_dev.argtypes = [vp, i32, i32, i32, cp, vp, i32, vp, vp]
         L.xtq_trellis_decode_dev.argtypes = [vp, i32, i32, i32, cp, vp, vp, vp]
         L.xtq_trellis_pack_dev.argtypes = [vp, i32, i32, vp, vp]
         L.xtq_trellis_unpack_dev.argtypes = [vp, i32, i32, vp, vp]
@@ -59,6 +60,7 @@ def lib():
         L.xtq_vit_strerror.argtypes = [i32]
         L.xtq_vit_strerror.restype = cp
         for fn in ("xtq_vit_init", "xtq_vit_run", "xtq_vit_run_k", "xtq_vit_tailbite_dev",
+                   "xtq_vit_viterbi_dev",
                    "xtq_trellis_decode_dev", "xtq_trellis_pack_dev",
                    "xtq_trellis_unpack_dev", "xtq_vit_get_lut"):
             getattr(L, fn).restype = i32
@@ -115,6 +117,40 @@ def tailbite(X: torch.Tensor, K: int, pivot: int, margin: int, code: str = "mul1
             tr.data_ptr() if tr is not None else None, _stream(X.device))
     _check("xtq_vit_tailbite_dev", rc)
     return st, tr
+
+
+def viterbi(X: torch.Tensor, K: int, overlap: torch.Tensor | None = None,
+            back_from: int | None = None, code: str = "mul1") -> torch.Tensor:
+    """One Viterbi run over X [nseq, T] fp32 (device), T <= 256.
+
+    Free run, or pinned to overlap [nseq] (s_0 >> K and s_{T-1} mod 2^(16-K));
+    returns int32 states [nseq, T], or [nseq] (the state at back_from).
+    Bit-exact with viterbi() (quantize.py:218-320) for V = 1, L = 16.
+    """
+    X = _dev_tensor(X, torch.float32, "X")
+    if X.dim() != 2 or not 1 <= X.shape[1] <= 256:
+        raise ValueError(f"X must be [nseq, T<=256], got {tuple(X.shape)}")
+    nseq, T = X.shape
+    bf = -1 if back_from is None else int(back_from)
+    if not -1 <= bf < T:
+        raise ValueError(f"back_from {back_from} outside [0, {T})")
+    ov = None
+    if overlap is not None:
+        ov = overlap.to(device=X.device, dtype=torch.int32).contiguous()
+        if ov.shape != (nseq,):
+            raise ValueError(f"overlap must be [{nseq}], got {tuple(ov.shape)}")
+        if nseq and (int(ov.min()) < 0 or int(ov.max()) >= (1 << (16 - K))):
+            raise ValueError("overlap values must lie in [0, 2^(16-K))")
+    out = torch.empty((nseq,) if bf >= 0 else (nseq, T), dtype=torch.int32, device=X.device)
+    if nseq == 0:
+        return out
+    with torch.cuda.device(X.device):
+        rc = lib().xtq_vit_viterbi_dev(
+            X.data_ptr(), nseq, T, int(K), code_name(code).encode(),
+            ov.data_ptr() if ov is not None else None, bf, out.data_ptr(),
+            _stream(X.device))
+    _check("xtq_vit_viterbi_dev", rc)
+    return out
 
 
 def decode(trellis: torch.Tensor, K: int, code: str = "mul1",

@@ -1,0 +1,587 @@
+#!/usr/bin/env python3
+"""quantize.py -- EXL3 trellis quantizer for one AMD Instinct MI355X (gfx950).
+
+Drop-in host module for the reference quantizer's public API
+(quantize/quantize.py of SergiioB/exl3xpu-mixedk): the same function names,
+argument meanings, defaults where they still make sense, return values and
+error behaviour.  The trellis work runs in hand-written HIP kernels
+(libexl3vit.so, include/exl3_vit.h) called through ctypes on torch-ROCm device
+tensors; there is no CPU Viterbi and no fallback -- every Viterbi, pack,
+unpack and decode call raises if the library or a HIP device is missing.
+
+Pipeline (reference citations are quantize.py:line):
+  incoherence   random signs + block-128 Hadamard on both sides     121-182
+  BlockLDLQ     block-LDL of the rotated damped Hessian, right-to-left
+                16-row sweep with error feedback                    419-437, 631-746
+  tail-biting   two-pass QTIP Viterbi per 16x16 tile (HIP)          323-354
+  format        packed trellis [k/16, n/16, 16K] int16, decode      357-415
+
+Orientation: public functions take nn.Linear W [out, in] and the input Gram
+H [in, in] in the original basis; internally W_i is [k=in, n=out].
+
+Backends: "hip" (default) runs the HIP kernels.  "torch" and "esimd", the
+reference's backend names, are accepted as aliases of "hip" so existing call
+sites keep working; the reference's per-launch "dual" comparator lives in the
+test-suite (tests/test_gpu_quantize.py), which compares every launch against
+the CPU oracle.  `compiled` and `batch` are accepted and ignored (the HIP path
+has no torch.compile step and chunks batches itself).
+"""
+from __future__ import annotations
+
+import math
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+import hip_backend as _hb  # noqa: E402
+
+BACKENDS = ("hip", "torch", "esimd")
+_DUAL_STATS: dict = {}
+
+
+# -------------------------------------------------------------- codebooks
+def _f16(bits) -> np.ndarray:
+    return np.asarray(bits).astype(np.uint16).view(np.float16)
+
+
+def _code_table(name: str, L: int) -> np.ndarray:
+    """fp32 decode table of a named V=1 code over all 2^L states
+    (the codes of quantize.py:56-87)."""
+    s = np.arange(1 << L, dtype=np.uint64)
+    if name == "exl3_mul1":
+        h = (s * 0x83DCD12D) & 0xFFFFFFFF
+        total = sum(((h >> sh) & 0xFF) for sh in (0, 8, 16, 24))
+        c1 = float(_f16(0x1EEE))
+        c2 = float(_f16(0xC931))
+        return ((1024 + total).astype(np.float64) * c1 + c2).astype(np.float16).astype(np.float32)
+    if name in ("exl3_3inst", "exl3_mcg"):
+        h = (s * 89226354 + 64248484) if name == "exl3_3inst" else (s * 0xCBAC1FED)
+        h = ((h & 0xFFFFFFFF) & 0x8FFF8FFF) ^ 0x3B603B60
+        a = _f16(h & 0xFFFF).astype(np.float64)
+        b = _f16(h >> 16).astype(np.float64)
+        return (a + b).astype(np.float16).astype(np.float32)
+    if name == "qtip_1mad":
+        h = (s * 34038481 + 76625530) & 0xFFFFFFFF
+        total = sum(((h >> sh) & 0xFF) for sh in (0, 8, 16, 24)).astype(np.float64)
+        return ((total - 510.0) / 147.800537109375).astype(np.float32)
+    raise KeyError(f"unknown local code {name!r}")
+
+
+def get_lut(code: str, L: int = 16, device=None) -> torch.Tensor:
+    """fp32 [2^L] decode table f(state) for the named code (quantize.py:90-97)."""
+    lut = torch.from_numpy(_code_table(code, L).copy())
+    return lut.to(device) if device is not None else lut
+
+
+_LUT_IDS: dict = {}
+
+
+def _kernel_code(lut: torch.Tensor, L: int) -> str:
+    """Library code name for a decode table (the kernels hold the tables)."""
+    if L != 16:
+        raise NotImplementedError("the HIP trellis kernels use the 16-bit state (L=16)")
+    lut = lut.detach().float().reshape(-1).cpu()
+    for name in ("exl3_mul1", "exl3_3inst", "exl3_mcg"):
+        ref = _LUT_IDS.get(name)
+        if ref is None:
+            ref = _LUT_IDS[name] = get_lut(name, 16)
+        if lut.shape == ref.shape and torch.equal(lut, ref):
+            return name
+    raise NotImplementedError(
+        "the HIP trellis kernels run the fp16-exact EXL3 codes exl3_mul1, exl3_3inst and "
+        "exl3_mcg; this decode table is none of them")
+
+
+# ------------------------------------------------------------ tile layout
+def tensor_core_perm() -> torch.Tensor:
+    """Sequence element t -> row-major position in the 16x16 [k, n] tile
+    (quantize.py:101-118): groups of eight elements walk row pairs
+    (r0, r0+1, r0+8, r0+9) in column c0 and then column c0+8."""
+    t = torch.arange(256)
+    g, e = t // 8, t % 8
+    row = (g % 4) * 2 + (e % 2) + 8 * ((e // 2) % 2)
+    col = g // 4 + 8 * (e // 4)
+    return (row * 16 + col).long()
+
+
+# ------------------------------------------------------------- incoherence
+_H128: dict = {}
+
+
+def hadamard128(device=None, dtype=torch.float32) -> torch.Tensor:
+    """Normalised 128x128 Sylvester Hadamard matrix (symmetric, H H = I)."""
+    key = (str(device), dtype)
+    if key not in _H128:
+        h = torch.ones(1, 1, dtype=torch.float64)
+        while h.shape[0] < 128:
+            h = torch.cat([torch.cat([h, h], 1), torch.cat([h, -h], 1)], 0)
+        _H128[key] = (h / math.sqrt(128)).to(dtype=dtype, device=device)
+    return _H128[key]
+
+
+def had_left(w: torch.Tensor, h: torch.Tensor) -> torch.Tensor:
+    """Block-128 Hadamard applied on the first (k) dim of w [k, n]."""
+    k, n = w.shape
+    assert k % 128 == 0
+    return torch.matmul(h, w.view(k // 128, 128, n)).view(k, n)
+
+
+def had_right(w: torch.Tensor, h: torch.Tensor) -> torch.Tensor:
+    """Block-128 Hadamard applied on the last (n) dim of w [k, n]."""
+    k, n = w.shape
+    assert n % 128 == 0
+    return torch.matmul(w.view(k, n // 128, 128), h).view(k, n)
+
+
+def to_inner(w_orig: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor,
+             h: torch.Tensor) -> torch.Tensor:
+    """W_orig [k, n] -> W_inner = B_k diag(1/suh) W diag(1/svh) B_n."""
+    w = w_orig / suh.float().unsqueeze(1)
+    w = w / svh.float().unsqueeze(0)
+    return had_right(had_left(w, h), h)
+
+
+def from_inner(w_inner: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor,
+               h: torch.Tensor) -> torch.Tensor:
+    """W_inner -> W_orig = diag(suh) B_k W_i B_n diag(svh)."""
+    w = had_left(w_inner, h) * suh.float().unsqueeze(1)
+    return had_right(w, h) * svh.float().unsqueeze(0)
+
+
+def rotate_hessian(H_x: torch.Tensor, suh: torch.Tensor, h: torch.Tensor) -> torch.Tensor:
+    """Inner-basis input Gram G = B diag(suh) H_x diag(suh) B."""
+    k = H_x.shape[0]
+    a = H_x.float() * suh.float().unsqueeze(0) * suh.float().unsqueeze(1)
+    return had_right(had_right(a.view(k, k), h).t().contiguous(), h)
+
+
+def sign_vec(n: int, seed: int, device=None) -> torch.Tensor:
+    """Deterministic Rademacher vector from torch's CPU generator."""
+    g = torch.Generator().manual_seed(seed)
+    return torch.where(torch.rand(n, generator=g) < 0.5, -1.0, 1.0).to(device)
+
+
+# ------------------------------------------------------------------ Viterbi
+def _check_viterbi_args(L: int, V: int, dtype, emit_mode: str):
+    if V != 1:
+        raise NotImplementedError("the HIP trellis kernels implement V=1 codes")
+    if dtype not in (torch.float32, None):
+        raise NotImplementedError("the bit-exact trellis path accumulates in float32")
+    if emit_mode != "sq":
+        raise NotImplementedError(
+            "emit_mode must be 'sq' (the addmm emit of the reference is not bit-exact)")
+    if L != 16:
+        raise NotImplementedError("the HIP trellis kernels use the 16-bit state (L=16)")
+
+
+def _on_gpu(X: torch.Tensor) -> torch.Tensor:
+    if X.is_cuda:
+        return X
+    if not torch.cuda.is_available():
+        raise RuntimeError("the trellis encoder needs a HIP device (none visible)")
+    return X.cuda()
+
+
+def viterbi(X: torch.Tensor, lut: torch.Tensor, K: int, L: int, V: int = 1,
+            overlap: torch.Tensor = None, dtype: torch.dtype = torch.float32,
+            back_from: int | None = None, compiled: bool = False,
+            emit_mode: str = "sq"):
+    """One trellis Viterbi run over X [T, B] (T <= 256), on the GPU.
+
+    Returns states [T, B] int64, or with back_from the state at step
+    back_from [B]; overlap [B] pins s_0 >> K and s_{T-1} mod 2^(L-K)
+    (quantize.py:218-320).  Results land on X's device.
+    """
+    _check_viterbi_args(L, V, dtype, emit_mode)
+    code = _hb.code_name(_kernel_code(lut, L))
+    Xg = _on_gpu(X).float()
+    st = _hb.viterbi(Xg.t().contiguous(), K, overlap=overlap, back_from=back_from,
+                     code=code)
+    st = st.long()
+    st = st if back_from is not None else st.t().contiguous()
+    return st.to(X.device)
+
+
+def quantize_seq_tailbite(X: torch.Tensor, lut: torch.Tensor, K: int, L: int,
+                          V: int = 1, dtype: torch.dtype = torch.float32,
+                          pivot: int | None = None, margin: int = 0,
+                          compiled: bool = False, emit_mode: str = "sq"):
+    """QTIP tail-biting Viterbi of X [256, B] -> states [256, B] int64 on the
+    GPU (quantize.py:323-354): pass 1 free on X rolled by pivot (truncated to
+    pivot+margin steps when margin > 0), wrap bits ov = s_pivot >> K, pass 2
+    pinned to ov."""
+    _check_viterbi_args(L, V, dtype, emit_mode)
+    T = X.shape[0]
+    if T != 256:
+        raise NotImplementedError("the HIP tail-biting encoder runs 256-step tiles")
+    if pivot is None:
+        pivot = T // 2
+    assert 0 <= pivot < T
+    code = _hb.code_name(_kernel_code(lut, L))
+    Xg = _on_gpu(X).float().t().contiguous()
+    st, _ = _hb.tailbite(Xg, K, int(pivot), int(margin), code=code)
+    return st.long().t().contiguous().to(X.device)
+
+
+# ------------------------------------------------------------ trellis format
+def pack_states(states: torch.Tensor, K: int, V: int = 1) -> torch.Tensor:
+    """states [ntiles, 256] -> int16 [ntiles, 16K] (quantize.py:360-378);
+    symbol t = s_t mod 2^K at stream bits [tK, (t+1)K) MSB first, 32-bit
+    words MSB first, stored as int16 halves, low half first."""
+    if V != 1:
+        raise NotImplementedError("V=1 only")
+    st = _on_gpu(states).to(torch.int32).reshape(-1, 256)
+    return _hb.pack(st, K).to(states.device)
+
+
+def unpack_states(trellis: torch.Tensor, K: int, V: int = 1) -> torch.Tensor:
+    """int16 [..., 16K] -> states [..., 256] int64 (quantize.py:381-402)."""
+    if V != 1:
+        raise NotImplementedError("V=1 only")
+    st = _hb.unpack(_on_gpu(trellis).reshape(-1, 16 * K), K)
+    return st.long().view(*trellis.shape[:-1], 256).to(trellis.device)
+
+
+def decode_trellis(trellis: torch.Tensor, lut: torch.Tensor, K: int, k: int, n: int,
+                   V: int = 1) -> torch.Tensor:
+    """int16 [k/16, n/16, 16K] -> W_inner fp32 [k, n] (quantize.py:405-415)."""
+    if V != 1:
+        raise NotImplementedError("V=1 only")
+    tk, tn, _ = trellis.shape
+    assert (16 * tk, 16 * tn) == (k, n), (trellis.shape, k, n)
+    code = _hb.code_name(_kernel_code(lut, 16))
+    return _hb.decode(_on_gpu(trellis), K, code=code).to(trellis.device)
+
+
+# ---------------------------------------------------------------- block LDL
+def block_LDL(H: torch.Tensor, b: int):
+    """QTIP block LDL (quantize.py:419-437): H = L D L^T with L unit-block
+    lower triangular (b x b identity diagonal blocks) and D block diagonal.
+    Raises torch's RuntimeError when H is not positive definite."""
+    n = H.shape[0]
+    assert n % b == 0
+    m = n // b
+    Lc = torch.linalg.cholesky(H)
+    blocks = torch.diagonal(Lc.reshape(m, b, m, b), dim1=0, dim2=2).permute(2, 0, 1)
+    D = blocks @ blocks.permute(0, 2, 1)
+    inv = torch.linalg.inv(blocks)
+    Lv = Lc.view(n, m, b)
+    for i in range(m):
+        Lv[:, i, :] = Lv[:, i, :] @ inv[i]
+    Lc = Lc.reshape(n, n).contiguous()
+    idx = torch.arange(m, device=Lc.device)
+    Lc.view(m, b, m, b)[idx, :, idx, :] = torch.eye(b, dtype=Lc.dtype, device=Lc.device)
+    return Lc, D
+
+
+# -------------------------------------------------------------- LDLQ sweep
+def _tile_targets(rows: torch.Tensor, perm: torch.Tensor) -> torch.Tensor:
+    """rows [16, n] of one 16-row block -> per-tile sequences [n/16, 256]
+    with x_t = tile[perm[t]] (quantize.py:684-686)."""
+    n = rows.shape[1]
+    tiles = rows.view(16, n // 16, 16).permute(1, 0, 2).reshape(n // 16, 256)
+    return tiles[:, perm].contiguous()
+
+
+def _launch(X: torch.Tensor, K: int, code: str, pivot: int, margin: int):
+    """One Viterbi launch: X [ntiles, 256] fp32 (device) -> (states int32,
+    trellis int16).  Tests wrap this to compare each launch with the oracle."""
+    return _hb.tailbite(X, K, pivot, margin, code=code, states=True, trellis=True)
+
+
+def ldlq_viterbi(Wq: torch.Tensor, Lfac: torch.Tensor | None, lut: torch.Tensor,
+                 K: int, L: int, buf_cols: int = 128, V: int = 1,
+                 batch: int = 0, dtype: torch.dtype = torch.float32,
+                 pivot: int | None = None, margin: int = 0,
+                 compiled: bool = False, progress=None,
+                 code: str | None = None, backend: str = "hip"):
+    """BlockLDLQ trellis quantization of W_i [k, n] (quantize.py:631-746).
+
+    Sweeps the 16-row blocks right to left.  Block i's targets are
+    W_i[rows i] + L[later, i]^T (W - What)[later] plus the lazily accumulated
+    feedback of earlier buffers (every buf_cols/16 blocks); each 16x16 tile of
+    the block is one tail-biting launch entry on the GPU.  Lfac None or all
+    zeros gives plain Viterbi.  Returns (hatW [k, n] fp32, states int64
+    [k/16, n/16, 256]) on Wq's device; the packed trellis of the sweep is left
+    in ldlq_viterbi.last_trellis ([k/16, n/16, 16K] int16, GPU).
+    """
+    if backend not in BACKENDS:
+        raise ValueError(f"backend {backend!r} not in {BACKENDS}")
+    _check_viterbi_args(L, V, dtype, "sq")
+    k, n = Wq.shape
+    assert k % 16 == 0 and n % 16 == 0
+    dev = Wq.device
+    gdev = _on_gpu(torch.empty(0)).device if not Wq.is_cuda else dev
+    kcode = _hb.code_name(_kernel_code(lut, L))
+    piv = 128 if pivot is None else int(pivot)
+    perm = tensor_core_perm().to(dev)
+    feedback = Lfac is not None and bool(Lfac.any())
+    Lf = Lfac.to(dev, Wq.dtype) if feedback else None
+    tk, tn = k // 16, n // 16
+
+    W_t = Wq.t().contiguous()                  # [n, k]
+    hatW_t = torch.zeros_like(W_t)
+    prod = torch.zeros(k, n, dtype=Wq.dtype, device=dev)
+    states = torch.empty(tk, tn, 256, dtype=torch.int32, device=gdev)
+    trellis = torch.empty(tk, tn, 16 * K, dtype=torch.int16, device=gdev)
+    per_buf = max(1, buf_cols // 16)
+    step_i = 0
+    for cur in range(tk, 0, -per_buf):
+        lo = max(0, cur - per_buf)
+        for i in range(cur - 1, lo - 1, -1):
+            c0, c1 = 16 * i, 16 * (i + 1)
+            rows = W_t[:, c0:c1].t().contiguous()          # [16, n]
+            if feedback:
+                if c1 < 16 * cur:
+                    err = (W_t[:, c1:16 * cur] - hatW_t[:, c1:16 * cur]).t()
+                    rows = rows + Lf[c1:16 * cur, c0:c1].t() @ err
+                rows = rows + prod[c0:c1, :]
+            X = _tile_targets(rows, perm)
+            st, tr = _launch(X.to(gdev), K, kcode, piv, int(margin))
+            states[i] = st
+            trellis[i] = tr
+            step_i += 512
+            if progress is not None:
+                progress(i, step_i)
+            # decoded block written back in [k, n] order: rows c0..c1 of What
+            blk = _hb.decode(tr.view(1, tn, 16 * K), K, code=kcode)   # [16, n]
+            hatW_t[:, c0:c1] = blk.to(dev).t()
+        if feedback and lo > 0:
+            err = (W_t[:, 16 * lo:16 * cur] - hatW_t[:, 16 * lo:16 * cur]).t()
+            prod += Lf[16 * lo:16 * cur, :].t() @ err
+    ldlq_viterbi.last_trellis = trellis
+    return hatW_t.t().contiguous(), states.long().to(dev)
+
+
+ldlq_viterbi.last_trellis = None
+
+
+# ---------------------------------------------------------------- top level
+def _factor_hessian(G: torch.Tensor):
+    """block_LDL of the damped rotated Gram with the reference's failure
+    policy (quantize.py:815-835): non-finite G raises; a non-SPD G is retried
+    in fp64 with +0, +0.1, +1.0 x mean(diag) extra damping."""
+    try:
+        Lfac, _ = block_LDL(G.float(), 16)
+        return Lfac
+    except RuntimeError:
+        if not torch.isfinite(G).all():
+            raise
+    Gd = G.double()
+    for extra in (0.0, 0.1, 1.0):
+        if extra:
+            Gd.diagonal().add_(extra * Gd.diagonal().mean())
+        try:
+            Lfac, _ = block_LDL(Gd.clone(), 16)
+            print(f"xtq_quant: block_LDL fallback used extra damping {extra} x mean diag",
+                  flush=True)
+            return Lfac
+        except RuntimeError:
+            if extra == 1.0:
+                raise
+    raise RuntimeError("unreachable")
+
+
+def quantize_linear(W: torch.Tensor, H_x: torch.Tensor | None, code: str = "exl3_mul1",
+                    K: int = 4, L: int = 16, V: int = 0, percdamp: float = 0.01,
+                    su_seed: int = 20261011, buf_cols: int = 128,
+                    use_ldlq: bool = True, device: str = "cpu",
+                    batch: int = 0, dtype: torch.dtype = torch.float32,
+                    margin: int = 0, compiled: bool = False, progress=None,
+                    backend: str = "hip", channel_scales: bool = False):
+    """Quantize one nn.Linear weight (quantize.py:750-875).
+
+    W [out, in]; H_x [in, in] undamped input Gram or None.  `device` is where
+    the torch work (incoherence, block-LDL, LDLQ feedback) runs -- pass the
+    GPU ("cuda") to keep the whole pipeline on the MI355X; the trellis
+    kernels always run on the GPU.  Returns a dict with W_hat [out, in] fp32,
+    trellis int16 [in/16, out/16, 16K], suh/svh fp16 and diagnostics.
+    channel_scales=True applies EXL3 1.4.2's per-channel scaling order.
+    """
+    m_out, k_in = W.shape
+    assert k_in % 128 == 0 and m_out % 128 == 0, (W.shape, "need k%128, n%128")
+    if backend not in BACKENDS:
+        raise ValueError(f"backend {backend!r} not in {BACKENDS}")
+    dev = torch.device(device)
+    lut = get_lut(code, L).to(torch.float32)
+    V = 1 if V == 0 else V
+    lut_rms = lut.double().square().mean().sqrt().float()
+
+    suh = sign_vec(k_in, su_seed, dev).half()
+    svh = sign_vec(m_out, su_seed + 1, dev).half()
+    h = hadamard128(dev, torch.float32)
+    W32 = W.float().to(dev).t().contiguous()          # [k, n]
+    if channel_scales:
+        su, sv = suh.float(), svh.float()
+        r_out = W32.square().mean(dim=0).sqrt()
+        rm = r_out.mean()
+        if rm > 1e-30:
+            r_out = r_out / rm
+        zero_out = r_out.abs() < 1e-30
+        r_out = torch.where(zero_out, torch.full_like(r_out, 0.1), r_out)
+        w = had_right(W32 / (sv * r_out).unsqueeze(0), h)
+        r_in = w.square().mean(dim=1).sqrt()
+        r_in = torch.where(r_in.abs() < 1e-30, torch.full_like(r_in, 0.1), r_in)
+        W_i = had_left(w / (su * r_in).unsqueeze(1), h)
+        svh_store = torch.where(zero_out, torch.zeros_like(r_out), r_out)
+    else:
+        W_i = to_inner(W32, suh, svh, h)
+    Wscale = W_i.square().mean().sqrt() / lut_rms
+    Wq = W_i / Wscale
+
+    Lfac = None
+    if use_ldlq and H_x is not None:
+        t0 = time.time()
+        G = rotate_hessian(H_x.float().to(dev), suh, h)
+        dead = G.diagonal() == 0
+        if dead.any():
+            G[dead, dead] = 1.0
+        G.diagonal().add_(percdamp * G.diagonal().mean())
+        Lfac = _factor_hessian(G).to(dev, Wq.dtype)
+        del G
+        if progress is not None:
+            progress("hinv", time.time() - t0)
+
+    hatWq, states = ldlq_viterbi(Wq, Lfac, lut, K, L, buf_cols=buf_cols, V=V,
+                                 batch=batch, dtype=dtype, margin=margin,
+                                 compiled=compiled, progress=progress,
+                                 code=code, backend=backend)
+    trellis = ldlq_viterbi.last_trellis                          # GPU
+    # bit-exact self-checks of the format round trip (quantize.py:848-853)
+    st_rt = _hb.unpack(trellis.view(-1, 16 * K), K)
+    assert torch.equal(st_rt.long().cpu(), states.reshape(-1, 256).cpu()), \
+        "pack/unpack round-trip broke state sequence"
+    hatW_d = decode_trellis(trellis, lut, K, k_in, m_out).to(dev)
+    assert torch.equal(hatW_d, hatWq), "decode != encoder output"
+    if channel_scales:
+        suh = (su * r_in * Wscale).half()
+        svh = (sv * svh_store).half()
+        W_hat = from_inner(hatW_d, suh, svh, h).t().contiguous()
+    else:
+        W_hat = from_inner(hatW_d * Wscale, suh, svh, h).t().contiguous()
+    return {
+        "W_hat": W_hat.cpu(),
+        "trellis": trellis.cpu(),
+        "suh": suh.cpu(), "svh": svh.cpu(),
+        "Wscale": float(Wscale), "lut_rms": float(lut_rms),
+        "code": code, "K": K, "L": L, "V": V, "use_ldlq": use_ldlq,
+        "channel_scales": channel_scales,
+    }
+
+
+def hessian_weighted_err(W: torch.Tensor, W_hat: torch.Tensor, H_x: torch.Tensor) -> float:
+    """Proxy loss tr(dW H dW^T) / tr(W H W^T), W [out, in] (quantize.py:878-885)."""
+    dW = (W_hat - W).float()
+    H = H_x.float()
+    num = torch.einsum("ij,jk,ik->", dW, H, dW)
+    den = torch.einsum("ij,jk,ik->", W.float(), H, W.float())
+    return float(num / den)
+
+
+def rel_mse(W: torch.Tensor, W_hat: torch.Tensor) -> float:
+    d = W_hat.float() - W.float()
+    return float(d.square().sum() / W.float().square().sum())
+
+
+def quantize(W_transformed: torch.Tensor, U_upper: torch.Tensor | None,
+             code: str, K: int, seed: int, L: int = 16,
+             dtype: torch.dtype = torch.float32,
+             backend: str = "hip", margin: int = 16, batch: int = 0,
+             su_mag: torch.Tensor | None = None,
+             sv_mag: torch.Tensor | None = None):
+    """Harness entry point (quantize.py:894-966).
+
+    W_transformed [out, in] fp32 already in the inner (incoherent) domain;
+    U_upper [in, in] the GPTQ-convention factor with U^T U = G^-1 (or None
+    for plain tail-biting Viterbi); seed picks the pass-1 pivot (seed mod 256).
+    su_mag/sv_mag fold per-channel magnitudes out before quantization and back
+    into W_hat.  Runs on W_transformed's device.  Returns (W_hat [out, in] fp32,
+    packed int16 [in/16, out/16, 16K], scale) with decode(packed) * scale ==
+    W_hat bit for bit (before the magnitude refold).
+    """
+    m_out, k_in = W_transformed.shape
+    assert k_in % 16 == 0 and m_out % 16 == 0, W_transformed.shape
+    lut = get_lut(code, L).float()
+    lut_rms = lut.double().square().mean().sqrt().float()
+    Wt = W_transformed.float()
+    folded = su_mag is not None or sv_mag is not None
+    if folded:
+        su_m = (torch.ones(k_in, dtype=Wt.dtype, device=Wt.device) if su_mag is None
+                else su_mag.float().to(Wt.device))
+        sv_m = (torch.ones(m_out, dtype=Wt.dtype, device=Wt.device) if sv_mag is None
+                else sv_mag.float().to(Wt.device))
+        Wt = Wt / (sv_m.unsqueeze(1) * su_m.unsqueeze(0))
+    Wq = Wt.t().contiguous()
+    scale = Wq.square().mean().sqrt() / lut_rms
+    Wq = Wq / scale
+    Lfac = None
+    if U_upper is not None:
+        Uu = U_upper.double()
+        eye = torch.eye(Uu.shape[0], dtype=Uu.dtype, device=Uu.device)
+        Ui = torch.linalg.solve_triangular(Uu, eye, upper=True)     # U^-1
+        Lfac, _ = block_LDL(Ui @ Ui.t(), 16)                         # G = U^-1 U^-T
+        Lfac = Lfac.float()
+    pivot = int(seed) % 256
+    hatWq, states = ldlq_viterbi(Wq, Lfac, lut, K, L, dtype=dtype, pivot=pivot,
+                                 margin=margin, code=code, backend=backend, batch=batch)
+    packed = ldlq_viterbi.last_trellis
+    st_rt = _hb.unpack(packed.view(-1, 16 * K), K).long()
+    assert torch.equal(st_rt.cpu(), states.reshape(-1, 256).cpu()), \
+        "pack/unpack round-trip broke state sequence"
+    W_hat = (hatWq * scale).t().contiguous()
+    hatW_rt = decode_trellis(packed, lut, K, k_in, m_out).to(hatWq.device) * scale
+    assert torch.equal(hatW_rt.t().contiguous(), W_hat), "decode != encoder"
+    if folded:
+        W_hat = W_hat * (sv_m.unsqueeze(1) * su_m.unsqueeze(0))
+    return W_hat, packed.to(W_transformed.device), float(scale)
+
+
+def prepare_incoherence(W: torch.Tensor, H_x: torch.Tensor | None = None,
+                        su_seed: int = 20261011,
+                        sv_seed: int | None = None,
+                        su_sign: torch.Tensor | None = None,
+                        sv_sign: torch.Tensor | None = None,
+                        channel_scales: bool = True,
+                        device: str = "cpu") -> dict:
+    """Incoherence transform in pieces for a harness that owns damping and the
+    U build (quantize.py:969-1058).  Returns Wt [out, in] (magnitudes folded,
+    Wscale not), the sign-only rotated undamped Gram G, signed magnitudes
+    suh/svh, raw magnitudes su_mag/sv_mag and the dead-output mask."""
+    m_out, k_in = W.shape
+    assert k_in % 128 == 0 and m_out % 128 == 0, (W.shape, "need %128 dims")
+    dev = torch.device(device)
+    h = hadamard128(dev, torch.float32)
+    su_s = (sign_vec(k_in, su_seed, dev).half() if su_sign is None
+            else su_sign.to(dev).half())
+    sv_s = (sign_vec(m_out, (su_seed + 1) if sv_seed is None else sv_seed, dev).half()
+            if sv_sign is None else sv_sign.to(dev).half())
+    W32 = W.float().to(dev).t().contiguous()
+    if channel_scales:
+        su, sv = su_s.float(), sv_s.float()
+        sv_mag = W32.square().mean(dim=0).sqrt()
+        rm = sv_mag.mean()
+        if rm > 1e-30:
+            sv_mag = sv_mag / rm
+        zero_out = sv_mag.abs() < 1e-30
+        sv_mag = torch.where(zero_out, torch.full_like(sv_mag, 0.1), sv_mag)
+        w = had_right(W32 / (sv * sv_mag).unsqueeze(0), h)
+        su_mag = w.square().mean(dim=1).sqrt()
+        su_mag = torch.where(su_mag.abs() < 1e-30, torch.full_like(su_mag, 0.1), su_mag)
+        W_i = had_left(w / (su * su_mag).unsqueeze(1), h)
+        suh = su * su_mag
+        svh = sv * torch.where(zero_out, torch.zeros_like(sv_mag), sv_mag)
+    else:
+        W_i = to_inner(W32, su_s, sv_s, h)
+        suh, svh = su_s.float(), sv_s.float()
+        su_mag = torch.ones(k_in, device=dev)
+        sv_mag = torch.ones(m_out, device=dev)
+        zero_out = torch.zeros(m_out, dtype=torch.bool, device=dev)
+    G = rotate_hessian(H_x.float().to(dev), su_s, h).cpu() if H_x is not None else None
+    return {"Wt": W_i.t().contiguous().cpu(), "G": G,
+            "suh": suh.cpu(), "svh": svh.cpu(),
+            "su_mag": su_mag.cpu(), "sv_mag": sv_mag.cpu(),
+            "zero_out": zero_out.cpu(), "channel_scales": channel_scales}

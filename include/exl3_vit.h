@@ -91,6 +91,21 @@ int xtq_vit_tailbite_dev(const float* dX, int nseq, int K, const char* code,
                          int16_t* d_trellis, void* stream);
 
 /*
+ * Device-pointer single Viterbi run: the HIP counterpart of viterbi()
+ * (quantize.py:218-320) with V = 1 and L = 16.
+ *   dX         [nseq][T] fp32 device, 1 <= T <= 256
+ *   d_overlap  [nseq] int32 device pin values in [0, 2^(16-K)), or NULL for a
+ *              free run; a pinned run pins s_0 >> K and s_{T-1} mod 2^(16-K)
+ *   back_from  -1: d_out is [nseq][T] int32, the full state sequence;
+ *              0 <= back_from < T: d_out is [nseq], the state at back_from
+ *              (links kept only after back_from, quantize.py:273-277,305-312)
+ * Synchronous on return, like xtq_vit_tailbite_dev.
+ */
+int xtq_vit_viterbi_dev(const float* dX, int nseq, int T, int K, const char* code,
+                        const int32_t* d_overlap, int back_from, int32_t* d_out,
+                        void* stream);
+
+/*
  * Device-pointer trellis decode: the HIP counterpart of decode_trellis
  * (quantize.py:405-415) and of exl3xpu's reconstruct (patch 0001:60-75).
  *   d_trellis [tk][tn][16K] int16 device

@@ -1,0 +1,80 @@
+"""The C-ABI library loads on any host, exports every symbol declared in
+include/exl3_vit.h, and rejects invalid arguments with the documented status
+codes before touching a device (quantize/viterbi_esimd.cpp:970-1005 codes)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from conftest import PKG, ROOT, load_golden
+
+HEADER = os.path.join(ROOT, "include", "exl3_vit.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    so = os.path.join(PKG, "lib", "libexl3vit.so")
+    if not os.path.exists(so):
+        subprocess.run(["make", "-s", "-C", PKG], check=True)
+    import hip_backend
+    return hip_backend.lib()
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(xtq_\w+)\s*\(", text)))
+
+
+def test_exports_every_declared_symbol(lib):
+    names = declared_functions()
+    assert len(names) >= 11
+    for name in names:
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", os.path.join(PKG, "lib", "libexl3vit.so")],
+                         capture_output=True, text=True, check=True).stdout
+    for name in names:
+        assert re.search(rf"\bT {name}\b", out), name
+
+
+def test_lut_export(lib):
+    out = np.empty(65536, np.float32)
+    assert lib.xtq_vit_get_lut(b"mul1", out.ctypes.data_as(ctypes.c_void_p)) == 0
+    np.testing.assert_array_equal(out, load_golden("lut_mul1.npz")["lut"])
+    assert lib.xtq_vit_get_lut(b"ih2x2", out.ctypes.data_as(ctypes.c_void_p)) == 8
+
+
+def test_status_codes_without_device(lib):
+    X = np.zeros((2, 256), np.float32)
+    st = np.zeros((2, 256), np.int32)
+    xp = X.ctypes.data_as(ctypes.c_void_p)
+    sp = st.ctypes.data_as(ctypes.c_void_p)
+    assert lib.xtq_vit_run(xp, 2, b"ih2x2", 0, 128, sp) == 8
+    assert lib.xtq_vit_run(xp, 2, b"bogus", 0, 128, sp) == 8
+    assert lib.xtq_vit_run(None, 2, b"mul1p", 0, 128, sp) == 12
+    assert lib.xtq_vit_run(xp, 0, b"mul1p", 0, 128, sp) == 6
+    assert lib.xtq_vit_run(xp, 2, b"mul1p", 0, 256, sp) == 10
+    assert lib.xtq_vit_run(xp, 2, b"mul1p", -1, 0, sp) == 10
+    assert lib.xtq_vit_run_k(xp, 2, 8, b"mul1", 0, 0, sp) == 9
+    assert lib.xtq_vit_run_k(xp, 2, 1, b"mul1", 0, 0, sp) == 9
+    fake = ctypes.c_void_p(16)          # never dereferenced: rejected first
+    assert lib.xtq_vit_tailbite_dev(fake, 4, 9, b"mul1", 0, 0, fake, None, None) == 9
+    assert lib.xtq_vit_tailbite_dev(fake, 4, 4, b"mul1", 0, 300, fake, None, None) == 10
+    assert lib.xtq_vit_tailbite_dev(fake, 4, 4, b"mul1", 0, 0, None, None, None) == 12
+    assert lib.xtq_vit_tailbite_dev(fake, 4, 4, b"qtip", 0, 0, fake, None, None) == 8
+    assert lib.xtq_vit_viterbi_dev(fake, 4, 300, 4, b"mul1", None, -1, fake, None) == 10
+    assert lib.xtq_vit_viterbi_dev(fake, 4, 256, 4, b"mul1", None, 256, fake, None) == 10
+    assert lib.xtq_trellis_decode_dev(fake, 1, 1, 8, b"mul1", fake, None, None) == 9
+    assert lib.xtq_trellis_pack_dev(fake, 1, 3, None, None) == 12
+    assert lib.xtq_vit_strerror(11) == b"NaN target"
+    assert lib.xtq_vit_strerror(99) == b"unknown status"
+
+
+def test_scratch_sizes(lib):
+    per = [lib.xtq_vit_scratch_per_seq(k) for k in range(2, 8)]
+    # 255 stored steps x (backpointer bytes per step)
+    assert per == [255 * 4096, 255 * 4096, 255 * 2048, 255 * 2048, 255 * 1024, 255 * 512]
+    assert lib.xtq_vit_scratch_per_seq(8) == -1

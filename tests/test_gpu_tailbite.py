@@ -50,6 +50,41 @@ def test_golden_tailbite(hb, K):
 
 
 @pytest.mark.parametrize("K", range(2, 8))
+def test_golden_viterbi_runs(hb, K):
+    """Single Viterbi runs equal the reference's viterbi(): free with full
+    traceback, truncated with back_from, and pinned to given overlaps."""
+    g = load_golden("tailbite.npz")
+    X = torch.from_numpy(g[f"X_K{K}"]).cuda()
+    print(f"case K={K} free", flush=True)
+    np.testing.assert_array_equal(hb.viterbi(X, K).cpu().numpy(), g[f"V_K{K}"])
+    print(f"case K={K} back_from", flush=True)
+    vb = hb.viterbi(X[:, :150].contiguous(), K, back_from=100)
+    np.testing.assert_array_equal(vb.cpu().numpy(), g[f"VB_K{K}"])
+    print(f"case K={K} pinned", flush=True)
+    ov = torch.from_numpy(g[f"VPov_K{K}"]).cuda()
+    np.testing.assert_array_equal(hb.viterbi(X, K, overlap=ov).cpu().numpy(), g[f"VP_K{K}"])
+
+
+@pytest.mark.parametrize("K", (2, 5, 7))
+def test_short_runs_vs_oracle(hb, oracle_mod, mul1_lut, K):
+    """Runs shorter than a tile (T = 1, 2, 17, 255) and pinned short runs."""
+    rng = np.random.default_rng(50 + K)
+    for T in (1, 2, 17, 255):
+        X = rng.standard_normal((5, T)).astype(np.float32)
+        print(f"case K={K} T={T}", flush=True)
+        got = hb.viterbi(torch.from_numpy(X).cuda(), K).cpu().numpy()
+        np.testing.assert_array_equal(got, oracle_mod.viterbi(X, mul1_lut, K, 16))
+        ov = rng.integers(0, 1 << (16 - K), 5).astype(np.int32)
+        got = hb.viterbi(torch.from_numpy(X).cuda(), K,
+                         overlap=torch.from_numpy(ov)).cpu().numpy()
+        np.testing.assert_array_equal(got, oracle_mod.viterbi(X, mul1_lut, K, 16, overlap=ov))
+        if T > 1:
+            got = hb.viterbi(torch.from_numpy(X).cuda(), K, back_from=T // 2).cpu().numpy()
+            np.testing.assert_array_equal(
+                got, oracle_mod.viterbi(X, mul1_lut, K, 16, back_from=T // 2))
+
+
+@pytest.mark.parametrize("K", range(2, 8))
 @pytest.mark.parametrize("group", ["1", "2", "4"])
 def test_oracle_random(hb, oracle_mod, mul1_lut, K, group, monkeypatch):
     """Random Gaussian and tie-heavy batches against the oracle, with each
