@@ -98,6 +98,44 @@ struct DevCtx {
 
 std::mutex g_mu;
 std::vector<DevCtx> g_dev;
+
+// Opt-in kernel timing: each forward/traceback launch is bracketed with HIP
+// events on its stream; elapsed times are folded in after the stream syncs.
+struct ProfPair { hipEvent_t a, b; int kind; double seq_steps; };
+bool g_prof = false;
+std::vector<ProfPair> g_prof_pending;
+double g_prof_ms[2] = {0.0, 0.0};
+long long g_prof_launches[2] = {0, 0};
+double g_prof_seq_steps = 0.0;
+
+// Records the start event of a timed launch (kind 0 forward, 1 traceback).
+int prof_begin(hipStream_t s, int kind, double seq_steps) {
+    if (!g_prof) return -1;
+    ProfPair p{nullptr, nullptr, kind, seq_steps};
+    if (hipEventCreate(&p.a) != hipSuccess || hipEventCreate(&p.b) != hipSuccess) return -1;
+    (void)hipEventRecord(p.a, s);
+    g_prof_pending.push_back(p);
+    return (int)g_prof_pending.size() - 1;
+}
+
+void prof_end(int idx, hipStream_t s) {
+    if (idx >= 0) (void)hipEventRecord(g_prof_pending[idx].b, s);
+}
+
+// Called after the stream has synchronised.
+void prof_collect() {
+    for (auto& p : g_prof_pending) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
+            g_prof_ms[p.kind] += ms;
+            g_prof_launches[p.kind] += 1;
+            if (p.kind == 0) g_prof_seq_steps += p.seq_steps;
+        }
+        (void)hipEventDestroy(p.a);
+        (void)hipEventDestroy(p.b);
+    }
+    g_prof_pending.clear();
+}
 bool g_env_read = false;
 long long g_maxseq = 1LL << 24;
 size_t g_maxbytes = (size_t)64 << 30;
@@ -230,6 +268,7 @@ int finish(DevCtx& cx, hipStream_t s) {
         fprintf(stderr, "xtq_vit run: %s\n", hipGetErrorString(hipGetLastError()));
         return 4;
     }
+    prof_collect();
     if (herr) {
         (void)hipMemset(cx.err, 0, sizeof(uint32_t));
         fprintf(stderr, "xtq_vit: NaN target\n");
@@ -265,20 +304,31 @@ int run_tailbite(DevCtx& cx, const float* dX, int nseq, int K, Code code, int ma
         hipError_t e;
         // Pass 1: free run over the sequence rolled right by pivot, n1 steps,
         // traced back to step pivot: ov = s_pivot >> K.
+        int pf = prof_begin(s, 0, (double)n * n1);
         e = xtq::launch_forward(K, x, xtq::kSteps, xtq::kSteps, n, lut, pivot, n1, pivot,
                                 nullptr, cx.bp, cx.send, cx.err, T, s);
-        if (e == hipSuccess)
+        prof_end(pf, s);
+        if (e == hipSuccess) {
+            pf = prof_begin(s, 1, 0.0);
             e = xtq::launch_traceback(K, cx.bp, n, cx.send, n1, pivot, K, cx.ov, nullptr,
                                       nullptr, s);
+            prof_end(pf, s);
+        }
         // Pass 2: run pinned to ov on the unrolled sequence, full traceback.
-        if (e == hipSuccess)
+        if (e == hipSuccess) {
+            pf = prof_begin(s, 0, (double)n * xtq::kSteps);
             e = xtq::launch_forward(K, x, xtq::kSteps, xtq::kSteps, n, lut, 0, xtq::kSteps, 0,
                                     cx.ov, cx.bp, cx.send, cx.err, T, s);
-        if (e == hipSuccess)
+            prof_end(pf, s);
+        }
+        if (e == hipSuccess) {
+            pf = prof_begin(s, 1, 0.0);
             e = xtq::launch_traceback(
                 K, cx.bp, n, cx.send, xtq::kSteps, 0, 0, nullptr,
                 d_states ? d_states + (size_t)c0 * xtq::kSteps : nullptr,
                 d_trellis ? d_trellis + (size_t)c0 * 16 * K : nullptr, s);
+            prof_end(pf, s);
+        }
         if (e != hipSuccess) {
             fprintf(stderr, "xtq_vit run: %s\n", hipGetErrorString(e));
             return 4;
@@ -515,6 +565,26 @@ int xtq_vit_get_lut(const char* code, float* out) {
 int64_t xtq_vit_scratch_per_seq(int K) {
     if (K < 2 || K > 7) return -1;
     return (int64_t)xtq::bp_tile_bytes(K);
+}
+
+int xtq_vit_prof_enable(int on) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_prof = on != 0;
+    return 0;
+}
+
+int xtq_vit_prof_read(double* fwd_ms, int64_t* fwd_launches, double* fwd_seq_steps,
+                      double* tb_ms, int64_t* tb_launches) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (fwd_ms) *fwd_ms = g_prof_ms[0];
+    if (fwd_launches) *fwd_launches = g_prof_launches[0];
+    if (fwd_seq_steps) *fwd_seq_steps = g_prof_seq_steps;
+    if (tb_ms) *tb_ms = g_prof_ms[1];
+    if (tb_launches) *tb_launches = g_prof_launches[1];
+    g_prof_ms[0] = g_prof_ms[1] = 0.0;
+    g_prof_launches[0] = g_prof_launches[1] = 0;
+    g_prof_seq_steps = 0.0;
+    return 0;
 }
 
 const char* xtq_vit_strerror(int rc) {

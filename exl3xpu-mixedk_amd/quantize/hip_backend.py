@@ -57,6 +57,12 @@ def lib():
         L.xtq_vit_get_lut.argtypes = [cp, vp]
         L.xtq_vit_scratch_per_seq.argtypes = [i32]
         L.xtq_vit_scratch_per_seq.restype = i64
+        L.xtq_vit_prof_enable.argtypes = [i32]
+        L.xtq_vit_prof_enable.restype = i32
+        dp = ctypes.POINTER(ctypes.c_double)
+        lp = ctypes.POINTER(ctypes.c_int64)
+        L.xtq_vit_prof_read.argtypes = [dp, lp, dp, dp, lp]
+        L.xtq_vit_prof_read.restype = i32
         L.xtq_vit_strerror.argtypes = [i32]
         L.xtq_vit_strerror.restype = cp
         for fn in ("xtq_vit_init", "xtq_vit_run", "xtq_vit_run_k", "xtq_vit_tailbite_dev",
@@ -209,3 +215,19 @@ def get_lut(code: str = "mul1") -> torch.Tensor:
 
 def scratch_per_seq(K: int) -> int:
     return int(lib().xtq_vit_scratch_per_seq(int(K)))
+
+
+def prof_enable(on: bool = True):
+    """Bracket every forward/traceback launch with HIP events (benchmarks)."""
+    lib().xtq_vit_prof_enable(1 if on else 0)
+
+
+def prof_read() -> dict:
+    """Totals since the last read: forward ms/launches/sequence-steps and
+    traceback ms/launches (xtq_vit_prof_read)."""
+    fm, ss, tm = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+    fl, tl = ctypes.c_int64(), ctypes.c_int64()
+    lib().xtq_vit_prof_read(ctypes.byref(fm), ctypes.byref(fl), ctypes.byref(ss),
+                            ctypes.byref(tm), ctypes.byref(tl))
+    return {"fwd_ms": fm.value, "fwd_launches": fl.value, "fwd_seq_steps": ss.value,
+            "tb_ms": tm.value, "tb_launches": tl.value}

@@ -131,6 +131,18 @@ int xtq_vit_get_lut(const char* code, float* out);
 /* Backpointer scratch bytes per sequence for K (sizing information). */
 int64_t xtq_vit_scratch_per_seq(int K);
 
+/*
+ * Kernel timing for benchmarks (no reference counterpart; the reference
+ * times whole calls with steady_clock, viterbi_esimd.cpp:869-880).  While
+ * enabled, every forward-DP and traceback launch is bracketed with HIP events
+ * on the stream it runs on.  xtq_vit_prof_read returns and resets the totals:
+ * forward milliseconds, forward launches, forward sequence-steps (sum of
+ * sequences x steps over the launches), traceback milliseconds and launches.
+ */
+int xtq_vit_prof_enable(int on);
+int xtq_vit_prof_read(double* fwd_ms, int64_t* fwd_launches, double* fwd_seq_steps,
+                      double* tb_ms, int64_t* tb_launches);
+
 /* Static description of a status code. */
 const char* xtq_vit_strerror(int rc);
 
