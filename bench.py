@@ -171,6 +171,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the CPU baseline, K sweep and end-to-end quantize")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
+                    help="after the timed steps, copy a buffer of BYTES bytes three times "
+                         "(a known-traffic kernel for scaling HBM counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; multi-GPU runs are out of scope "
@@ -200,6 +203,15 @@ def main():
     hb.prof_enable(False)
     prof = hb.prof_read()
     log(f"timed {args.steps} steps: {dt:.3f} s")
+    if args.calibrate_copy:
+        src = torch.empty(args.calibrate_copy // 4, dtype=torch.float32, device="cuda")
+        src.fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        log(f"calibration copies of {args.calibrate_copy} bytes done")
     tps = n * args.steps / dt
 
     fwd_avg_ms = prof["fwd_ms"] / max(1, prof["fwd_launches"])
