@@ -129,13 +129,22 @@ def k_sweep(X: torch.Tensor, n: int = 65536):
     for K in range(2, 8):
         run_step(Xs[:4096], K)
         torch.cuda.synchronize()
+        hb.prof_read()
+        hb.prof_enable(True)
         t0 = time.perf_counter()
         run_step(Xs, K)
         torch.cuda.synchronize()
         dt = time.perf_counter() - t0
+        hb.prof_enable(False)
+        p = hb.prof_read()
+        kfrac = (OPS_PER_STATE_STEP * 65536 * p["fwd_seq_steps"] / (p["fwd_ms"] * 1e-3)
+                 / VALU_PEAK) if p["fwd_ms"] > 0 else None
         out[str(K)] = {"tiles_per_s": round(n / dt, 1),
-                       "valu_frac": round(n / dt * OPS_PER_STATE_STEP * 65536 * 512 / VALU_PEAK, 4)}
-        log(f"k_sweep K={K}: {n / dt:,.0f} tiles/s")
+                       "valu_frac": round(n / dt * OPS_PER_STATE_STEP * 65536 * 512 / VALU_PEAK, 4),
+                       "fwd_kernel_frac": round(kfrac, 4) if kfrac else None,
+                       "traceback_ms": round(p["tb_ms"], 2)}
+        log(f"k_sweep K={K}: {n / dt:,.0f} tiles/s, forward kernel "
+            f"{100 * (kfrac or 0):.1f}% of VALU peak")
     return out
 
 

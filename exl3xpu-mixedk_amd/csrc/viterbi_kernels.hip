@@ -88,6 +88,41 @@ __device__ __forceinline__ double kmin_xor(double k, int m) {
     return kmin(k, key_of(plo, __uint_as_float(phi)));
 }
 
+// Min with the neighbour lane (lane ^ 1) through a DPP quad permutation
+// [1,0,3,2]: two v_mov_b32_dpp and one v_min_f64, no LDS round trip.
+__device__ __forceinline__ double kmin_xor1(double k) {
+    const int lo = (int)key_lo(k), hi = (int)__float_as_uint(key_cost(k));
+    const uint32_t plo = (uint32_t)__builtin_amdgcn_mov_dpp(lo, 0xB1, 0xF, 0xF, false);
+    const uint32_t phi = (uint32_t)__builtin_amdgcn_mov_dpp(hi, 0xB1, 0xF, 0xF, false);
+    return kmin(k, key_of(plo, __uint_as_float(phi)));
+}
+
+// Byte address of a __shared__ location in the LDS aperture.
+__device__ __forceinline__ uint32_t lds_addr(const float* p) {
+    return (uint32_t)(size_t)(__attribute__((address_space(3))) const float*)(p);
+}
+
+// Stores the cost halves of two keys to dwords D and D+1 after `addr` with
+// one ds_write2_b32 straight from the key registers (a vector store of the
+// four costs would first gather them into consecutive VGPRs).  The compiler
+// does not see this store: the caller waits with lgkmcnt(0) before the
+// barrier that publishes it.
+template <int D>
+__device__ __forceinline__ void lds_store_cost2(uint32_t addr, double k0, double k1) {
+    asm volatile("ds_write2_b32 %0, %1, %2 offset0:%3 offset1:%4"
+                 :
+                 : "v"(addr), "v"(key_cost(k0)), "v"(key_cost(k1)), "i"(D), "i"(D + 1)
+                 : "memory");
+}
+
+template <int C, int c = 0>
+__device__ __forceinline__ void lds_store_costs(uint32_t addr, const double* run) {
+    if constexpr (c < C) {
+        lds_store_cost2<c>(addr, run[c], run[c + 1]);
+        lds_store_costs<C, c + 2>(addr, run);
+    }
+}
+
 // Backpointer of group j in one step's row.
 template <int K>
 __device__ __forceinline__ int bp_lookup(const uint8_t* row, int j) {
@@ -223,19 +258,22 @@ __global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
                     }
                 }
             }
-            if constexpr (G::HALF) run[0] = kmin_xor(run[0], 1);  // merge the two halves
+            if constexpr (G::HALF) run[0] = kmin_xor1(run[0]);  // merge the two halves
 
             uint8_t* bpq = bp + (size_t)q * ((size_t)kSlots * G::BPSTEP);
             if (i + 1 < nsteps) {
                 float* bnext = bbuf[tt][(i + 1) & 1] + jbase;
-                if constexpr (G::C % 4 == 0) {
+                if constexpr (G::C == 2 || G::C == 4) {
+                    lds_store_costs<G::C>(lds_addr(bnext), run);
+                } else if constexpr (G::C % 4 == 0) {
+                    // 8 or 16 costs per lane: 16-byte stores keep each lane's
+                    // bytes contiguous (dword pairs at a 32/64-byte lane
+                    // stride would pile onto a few LDS banks).
 #pragma unroll
                     for (int c = 0; c < G::C; c += 4)
                         *(float4*)(bnext + c) =
                             make_float4(key_cost(run[c]), key_cost(run[c + 1]),
                                         key_cost(run[c + 2]), key_cost(run[c + 3]));
-                } else if constexpr (G::C == 2) {
-                    *(float2*)bnext = make_float2(key_cost(run[0]), key_cost(run[1]));
                 } else {
                     if (!G::HALF || (tid & 1) == 0) bnext[0] = key_cost(run[0]);
                 }
@@ -244,11 +282,15 @@ __global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
                         if ((tid & 1) == 0)
                             bpq[(size_t)i * G::BPSTEP + jbase] = (uint8_t)(key_lo(run[0]) & 0x7F);
                     } else {
+                        // Funnel-shift each group's K index bits (the low bits
+                        // of its key tag) in from the top, one v_alignbit_b32
+                        // per group; group c ends at bits [cK, (c+1)K).
                         typedef typename UnitT<G::UNIT>::type unit_t;
                         uint32_t bits = 0;
 #pragma unroll
                         for (int c = 0; c < G::C; ++c)
-                            bits |= (key_lo(run[c]) & (uint32_t)(G::NC - 1)) << (c * K);
+                            bits = __builtin_amdgcn_alignbit(key_lo(run[c]), bits, (uint32_t)K);
+                        if constexpr (G::BITS < 32) bits >>= (32 - G::BITS);
                         *(unit_t*)(bpq + (size_t)i * G::BPSTEP + (size_t)tid * G::UNIT) =
                             (unit_t)bits;
                     }
@@ -293,6 +335,9 @@ __global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
                 __syncthreads();
             }
         }
+        // The cost stores above are inline ds_write2_b32 the compiler does
+        // not track: complete them before the barrier publishes b_{i+1}.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __syncthreads();
     }
 }
