@@ -94,6 +94,10 @@ struct DevCtx {
     int32_t* hs = nullptr;
     size_t host_cap = 0;
     size_t owned = 0;          // device bytes held
+    // Recorded on the stream of the last call that used the scratch above;
+    // the next call waits for it on its own stream, and growing the scratch
+    // waits for it on the host before freeing.
+    hipEvent_t last = nullptr;
 };
 
 std::mutex g_mu;
@@ -172,6 +176,8 @@ int dev_init(int dev) {
     }
     if (hipMalloc((void**)&cx.err, sizeof(uint32_t)) != hipSuccess) return 2;
     if (hipMemset(cx.err, 0, sizeof(uint32_t)) != hipSuccess) return 1;
+    if (hipEventCreateWithFlags(&cx.last, hipEventDisableTiming) != hipSuccess) return 1;
+    if (hipEventRecord(cx.last, 0) != hipSuccess) return 1;
     cx.owned = kNumCodes * 65536 * sizeof(uint16_t) + 256;
     cx.ready = true;
     return 0;
@@ -239,6 +245,11 @@ int chunk_size(const DevCtx& cx, int K, int nseq) {
 // Grows the backpointer/final-state scratch for `chunk` sequences of K.
 int reserve_scratch(DevCtx& cx, int K, int chunk) {
     const size_t per = xtq::bp_tile_bytes(K);
+    // A stream-ordered call may still be using the buffers about to be
+    // replaced.
+    if (((size_t)chunk * per > cx.bp_cap || (size_t)chunk > cx.seq_cap) &&
+        hipEventSynchronize(cx.last) != hipSuccess)
+        return 4;
     // Device bytes this call adds to what the library already holds.
     size_t add = 0;
     if ((size_t)chunk * per > cx.bp_cap) add += (size_t)chunk * per - cx.bp_cap;
@@ -289,11 +300,25 @@ int pick_group(const DevCtx& cx, int K, int n) {
     return T;
 }
 
+// Orders a call's use of the library scratch after the previous call's.
+int scratch_begin(DevCtx& cx, hipStream_t s) {
+    return hipStreamWaitEvent(s, cx.last, 0) == hipSuccess ? 0 : 4;
+}
+
+// Marks the end of a call's scratch use; a synchronous call then waits for
+// its stream and reports the NaN flag.
+int scratch_end(DevCtx& cx, hipStream_t s, bool sync) {
+    if (hipEventRecord(cx.last, s) != hipSuccess) return 4;
+    return sync ? finish(cx, s) : 0;
+}
+
 // The two-pass tail-biting schedule over device buffers (quantize.py:323-354).
 int run_tailbite(DevCtx& cx, const float* dX, int nseq, int K, Code code, int margin,
-                 int pivot, int32_t* d_states, int16_t* d_trellis, hipStream_t s) {
+                 int pivot, int32_t* d_states, int16_t* d_trellis, hipStream_t s,
+                 bool sync = true) {
     const int chunk = chunk_size(cx, K, nseq);
     int rc = reserve_scratch(cx, K, chunk);
+    if (!rc) rc = scratch_begin(cx, s);
     if (rc) return rc;
     const int n1 = (margin > 0 && pivot + margin < xtq::kSteps) ? pivot + margin : xtq::kSteps;
     const uint16_t* lut = cx.lut16[code];
@@ -334,7 +359,7 @@ int run_tailbite(DevCtx& cx, const float* dX, int nseq, int K, Code code, int ma
             return 4;
         }
     }
-    return finish(cx, s);
+    return scratch_end(cx, s, sync);
 }
 
 // One Viterbi run (quantize.py:218-320) over device buffers: free or pinned,
@@ -343,6 +368,7 @@ int run_viterbi(DevCtx& cx, const float* dX, int nseq, int T, int K, Code code,
                 const int32_t* d_ov, int back_from, int32_t* d_out, hipStream_t s) {
     const int chunk = chunk_size(cx, K, nseq);
     int rc = reserve_scratch(cx, K, chunk);
+    if (!rc) rc = scratch_begin(cx, s);
     if (rc) return rc;
     const uint16_t* lut = cx.lut16[code];
     const int stop = back_from >= 0 ? back_from : 0;
@@ -365,7 +391,7 @@ int run_viterbi(DevCtx& cx, const float* dX, int nseq, int T, int K, Code code,
             return 4;
         }
     }
-    return finish(cx, s);
+    return scratch_end(cx, s, true);
 }
 
 // Host-pointer tail-bite: stage X, run, copy the states back.
@@ -390,6 +416,8 @@ int run_host(const float* X, int nseq, int K, Code code, int margin, int pivot,
             rc = 5;
         }
         size_t c1 = cx.host_cap, c2 = cx.host_cap;
+        if (!rc && (size_t)nseq > cx.host_cap && hipEventSynchronize(cx.last) != hipSuccess)
+            rc = 4;
         if (!rc && (size_t)nseq > cx.host_cap) {
             if (grow(&cx.hx, &c1, (size_t)nseq * xtq::kSteps, sizeof(float), &cx.owned) ||
                 grow(&cx.hs, &c2, (size_t)nseq * xtq::kSteps, sizeof(int32_t), &cx.owned)) {
@@ -460,8 +488,13 @@ int xtq_vit_run_k(const float* X, int nseq, int K, const char* code, int margin,
     return run_host(X, nseq, K, c, margin, pivot, out);
 }
 
-int xtq_vit_tailbite_dev(const float* dX, int nseq, int K, const char* code, int margin,
-                         int pivot, int32_t* d_states, int16_t* d_trellis, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Shared body of the synchronous and stream-ordered device tail-bite entries.
+int tailbite_dev(const float* dX, int nseq, int K, const char* code, int margin, int pivot,
+                 int32_t* d_states, int16_t* d_trellis, void* stream, bool sync) {
     std::lock_guard<std::mutex> lk(g_mu);
     if (!dX || (!d_states && !d_trellis)) return 12;
     Code c;
@@ -475,7 +508,31 @@ int xtq_vit_tailbite_dev(const float* dX, int nseq, int K, const char* code, int
     rc = dev_init(dev);
     if (rc) return rc;
     return run_tailbite(g_dev[dev], dX, nseq, K, c, margin, pivot, d_states, d_trellis,
-                        (hipStream_t)stream);
+                        (hipStream_t)stream, sync);
+}
+
+}  // namespace
+
+extern "C" {
+
+int xtq_vit_tailbite_dev(const float* dX, int nseq, int K, const char* code, int margin,
+                         int pivot, int32_t* d_states, int16_t* d_trellis, void* stream) {
+    return tailbite_dev(dX, nseq, K, code, margin, pivot, d_states, d_trellis, stream, true);
+}
+
+int xtq_vit_tailbite_dev_async(const float* dX, int nseq, int K, const char* code,
+                               int margin, int pivot, int32_t* d_states, int16_t* d_trellis,
+                               void* stream) {
+    return tailbite_dev(dX, nseq, K, code, margin, pivot, d_states, d_trellis, stream, false);
+}
+
+int xtq_vit_status_dev(void* stream) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    int dev = 0;
+    if (current_device(&dev)) return 1;
+    int rc = dev_init(dev);
+    if (rc) return rc;
+    return finish(g_dev[dev], (hipStream_t)stream);
 }
 
 int xtq_vit_viterbi_dev(const float* dX, int nseq, int T, int K, const char* code,
@@ -513,7 +570,6 @@ int xtq_trellis_decode_dev(const int16_t* d_trellis, int tk, int tn, int K, cons
     if (rc) return rc;
     hipError_t e = xtq::launch_decode(K, d_trellis, tk, tn, g_dev[dev].lut16[c], d_out_f32,
                                       d_out_f16, (hipStream_t)stream);
-    if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
     if (e != hipSuccess) {
         fprintf(stderr, "xtq_vit decode: %s\n", hipGetErrorString(e));
         return 4;
@@ -528,7 +584,6 @@ int xtq_trellis_pack_dev(const int32_t* d_states, int nt, int K, int16_t* d_trel
     if (K < 2 || K > 7) return 9;
     if (nt <= 0) return 6;
     hipError_t e = xtq::launch_pack(K, d_states, nt, d_trellis, (hipStream_t)stream);
-    if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
     if (e != hipSuccess) {
         fprintf(stderr, "xtq_vit pack: %s\n", hipGetErrorString(e));
         return 4;
@@ -543,7 +598,6 @@ int xtq_trellis_unpack_dev(const int16_t* d_trellis, int nt, int K, int32_t* d_s
     if (K < 2 || K > 7) return 9;
     if (nt <= 0) return 6;
     hipError_t e = xtq::launch_unpack(K, d_trellis, nt, d_states, (hipStream_t)stream);
-    if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
     if (e != hipSuccess) {
         fprintf(stderr, "xtq_vit unpack: %s\n", hipGetErrorString(e));
         return 4;

@@ -50,6 +50,8 @@ def lib():
         L.xtq_vit_run.argtypes = [vp, i32, cp, i32, i32, vp]
         L.xtq_vit_run_k.argtypes = [vp, i32, i32, cp, i32, i32, vp]
         L.xtq_vit_tailbite_dev.argtypes = [vp, i32, i32, cp, i32, i32, vp, vp, vp]
+        L.xtq_vit_tailbite_dev_async.argtypes = [vp, i32, i32, cp, i32, i32, vp, vp, vp]
+        L.xtq_vit_status_dev.argtypes = [vp]
         L.xtq_vit_viterbi_dev.argtypes = [vp, i32, i32, i32, cp, vp, i32, vp, vp]
         L.xtq_trellis_decode_dev.argtypes = [vp, i32, i32, i32, cp, vp, vp, vp]
         L.xtq_trellis_pack_dev.argtypes = [vp, i32, i32, vp, vp]
@@ -66,7 +68,7 @@ def lib():
         L.xtq_vit_strerror.argtypes = [i32]
         L.xtq_vit_strerror.restype = cp
         for fn in ("xtq_vit_init", "xtq_vit_run", "xtq_vit_run_k", "xtq_vit_tailbite_dev",
-                   "xtq_vit_viterbi_dev",
+                   "xtq_vit_tailbite_dev_async", "xtq_vit_status_dev", "xtq_vit_viterbi_dev",
                    "xtq_trellis_decode_dev", "xtq_trellis_pack_dev",
                    "xtq_trellis_unpack_dev", "xtq_vit_get_lut"):
             getattr(L, fn).restype = i32
@@ -101,12 +103,14 @@ def _stream(dev: torch.device) -> int:
 
 
 def tailbite(X: torch.Tensor, K: int, pivot: int, margin: int, code: str = "mul1",
-             states: bool = True, trellis: bool = False):
+             states: bool = True, trellis: bool = False, sync: bool = True):
     """Tail-biting encode of X [nseq, 256] fp32 (device).
 
     Returns (states int32 [nseq, 256] or None, trellis int16 [nseq, 16K] or
     None), both on X's device.  Bit-exact with quantize_seq_tailbite
     (quantize.py:323-354) given the same targets, pivot and margin.
+    sync=False only enqueues the work on the current stream; a NaN target is
+    then reported by the next status() call instead of raising here.
     """
     X = _dev_tensor(X, torch.float32, "X")
     if X.dim() != 2 or X.shape[1] != 256:
@@ -116,13 +120,22 @@ def tailbite(X: torch.Tensor, K: int, pivot: int, margin: int, code: str = "mul1
     tr = torch.empty(nseq, 16 * K, dtype=torch.int16, device=X.device) if trellis else None
     if nseq == 0:
         return st, tr
+    fn = "xtq_vit_tailbite_dev" if sync else "xtq_vit_tailbite_dev_async"
     with torch.cuda.device(X.device):
-        rc = lib().xtq_vit_tailbite_dev(
+        rc = getattr(lib(), fn)(
             X.data_ptr(), nseq, int(K), code_name(code).encode(), int(margin), int(pivot),
             st.data_ptr() if st is not None else None,
             tr.data_ptr() if tr is not None else None, _stream(X.device))
-    _check("xtq_vit_tailbite_dev", rc)
+    _check(fn, rc)
     return st, tr
+
+
+def status(device=None):
+    """Wait for the current stream of `device` and raise HipViterbiError
+    (rc 11) if a stream-ordered encode met a NaN target since the last check."""
+    dev = torch.device("cuda") if device is None else torch.device(device)
+    with torch.cuda.device(dev):
+        _check("xtq_vit_status_dev", lib().xtq_vit_status_dev(_stream(dev)))
 
 
 def viterbi(X: torch.Tensor, K: int, overlap: torch.Tensor | None = None,

@@ -270,8 +270,13 @@ def block_LDL(H: torch.Tensor, b: int):
     D = blocks @ blocks.permute(0, 2, 1)
     inv = torch.linalg.inv(blocks)
     Lv = Lc.view(n, m, b)
-    for i in range(m):
-        Lv[:, i, :] = Lv[:, i, :] @ inv[i]
+    if Lc.is_cuda:
+        # one batched product on the GPU (m launches of a 16-wide product
+        # would dominate); each entry is the same length-b dot product
+        Lv.copy_(torch.bmm(Lv.permute(1, 0, 2), inv).permute(1, 0, 2))
+    else:
+        for i in range(m):
+            Lv[:, i, :] = Lv[:, i, :] @ inv[i]
     Lc = Lc.reshape(n, n).contiguous()
     idx = torch.arange(m, device=Lc.device)
     Lc.view(m, b, m, b)[idx, :, idx, :] = torch.eye(b, dtype=Lc.dtype, device=Lc.device)
@@ -289,8 +294,11 @@ def _tile_targets(rows: torch.Tensor, perm: torch.Tensor) -> torch.Tensor:
 
 def _launch(X: torch.Tensor, K: int, code: str, pivot: int, margin: int):
     """One Viterbi launch: X [ntiles, 256] fp32 (device) -> (states int32,
-    trellis int16).  Tests wrap this to compare each launch with the oracle."""
-    return _hb.tailbite(X, K, pivot, margin, code=code, states=True, trellis=True)
+    trellis int16), enqueued on the current stream without waiting (the sweep
+    checks the NaN status once at its end).  Tests wrap this to compare each
+    launch with the oracle."""
+    return _hb.tailbite(X, K, pivot, margin, code=code, states=True, trellis=True,
+                        sync=False)
 
 
 def ldlq_viterbi(Wq: torch.Tensor, Lfac: torch.Tensor | None, lut: torch.Tensor,
@@ -353,6 +361,7 @@ def ldlq_viterbi(Wq: torch.Tensor, Lfac: torch.Tensor | None, lut: torch.Tensor,
         if feedback and lo > 0:
             err = (W_t[:, 16 * lo:16 * cur] - hatW_t[:, 16 * lo:16 * cur]).t()
             prod += Lf[16 * lo:16 * cur, :].t() @ err
+    _hb.status(gdev)                 # NaN targets anywhere in the sweep raise here
     ldlq_viterbi.last_trellis = trellis
     return hatW_t.t().contiguous(), states.long().to(dev)
 
@@ -451,12 +460,14 @@ def quantize_linear(W: torch.Tensor, H_x: torch.Tensor | None, code: str = "exl3
                                  compiled=compiled, progress=progress,
                                  code=code, backend=backend)
     trellis = ldlq_viterbi.last_trellis                          # GPU
-    # bit-exact self-checks of the format round trip (quantize.py:848-853)
+    # bit-exact self-checks of the format round trip (quantize.py:848-853),
+    # compared where the trellis lives
     st_rt = _hb.unpack(trellis.view(-1, 16 * K), K)
-    assert torch.equal(st_rt.long().cpu(), states.reshape(-1, 256).cpu()), \
+    assert torch.equal(st_rt, states.reshape(-1, 256).to(st_rt.device, torch.int32)), \
         "pack/unpack round-trip broke state sequence"
-    hatW_d = decode_trellis(trellis, lut, K, k_in, m_out).to(dev)
-    assert torch.equal(hatW_d, hatWq), "decode != encoder output"
+    hatW_g = _hb.decode(trellis, K, code=_hb.code_name(code))
+    assert torch.equal(hatW_g, hatWq.to(hatW_g.device)), "decode != encoder output"
+    hatW_d = hatW_g.to(dev)
     if channel_scales:
         suh = (su * r_in * Wscale).half()
         svh = (sv * svh_store).half()
@@ -529,8 +540,8 @@ def quantize(W_transformed: torch.Tensor, U_upper: torch.Tensor | None,
     hatWq, states = ldlq_viterbi(Wq, Lfac, lut, K, L, dtype=dtype, pivot=pivot,
                                  margin=margin, code=code, backend=backend, batch=batch)
     packed = ldlq_viterbi.last_trellis
-    st_rt = _hb.unpack(packed.view(-1, 16 * K), K).long()
-    assert torch.equal(st_rt.cpu(), states.reshape(-1, 256).cpu()), \
+    st_rt = _hb.unpack(packed.view(-1, 16 * K), K)
+    assert torch.equal(st_rt, states.reshape(-1, 256).to(st_rt.device, torch.int32)), \
         "pack/unpack round-trip broke state sequence"
     W_hat = (hatWq * scale).t().contiguous()
     hatW_rt = decode_trellis(packed, lut, K, k_in, m_out).to(hatWq.device) * scale

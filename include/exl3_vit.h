@@ -91,6 +91,27 @@ int xtq_vit_tailbite_dev(const float* dX, int nseq, int K, const char* code,
                          int16_t* d_trellis, void* stream);
 
 /*
+ * Stream-ordered variant of xtq_vit_tailbite_dev (no reference counterpart:
+ * the reference's run is synchronous, viterbi_esimd.cpp:970-1005).  Returns
+ * once the work is enqueued on `stream`; the outputs are valid in stream
+ * order.  A NaN target is not reported here: it sets a per-device flag that
+ * xtq_vit_status_dev reads.  For the BlockLDLQ sweep, which issues one
+ * encode per 16-row block and must not wait on the host between blocks.
+ * Calls on different streams are ordered among themselves by the library
+ * (they share its backpointer scratch).
+ */
+int xtq_vit_tailbite_dev_async(const float* dX, int nseq, int K, const char* code,
+                               int margin, int pivot, int32_t* d_states,
+                               int16_t* d_trellis, void* stream);
+
+/*
+ * Waits for `stream` and reports the NaN flag that stream-ordered encodes
+ * set since the last status or synchronous call: 0, or 11 (the flag is then
+ * cleared), or 4 on a HIP error.
+ */
+int xtq_vit_status_dev(void* stream);
+
+/*
  * Device-pointer single Viterbi run: the HIP counterpart of viterbi()
  * (quantize.py:218-320) with V = 1 and L = 16.
  *   dX         [nseq][T] fp32 device, 1 <= T <= 256
@@ -111,6 +132,8 @@ int xtq_vit_viterbi_dev(const float* dX, int nseq, int T, int K, const char* cod
  *   d_trellis [tk][tn][16K] int16 device
  *   d_out_f32 [16tk][16tn] fp32 device, or NULL
  *   d_out_f16 [16tk][16tn] fp16 (bit patterns) device, or NULL
+ * Stream-ordered: returns once the kernel is enqueued on `stream` (as do
+ * the pack and unpack entries below).
  */
 int xtq_trellis_decode_dev(const int16_t* d_trellis, int tk, int tn, int K,
                            const char* code, float* d_out_f32, uint16_t* d_out_f16,

@@ -65,6 +65,9 @@ def test_status_codes_without_device(lib):
     assert lib.xtq_vit_tailbite_dev(fake, 4, 4, b"mul1", 0, 300, fake, None, None) == 10
     assert lib.xtq_vit_tailbite_dev(fake, 4, 4, b"mul1", 0, 0, None, None, None) == 12
     assert lib.xtq_vit_tailbite_dev(fake, 4, 4, b"qtip", 0, 0, fake, None, None) == 8
+    assert lib.xtq_vit_tailbite_dev_async(fake, 4, 9, b"mul1", 0, 0, fake, None, None) == 9
+    assert lib.xtq_vit_tailbite_dev_async(fake, 0, 4, b"mul1", 0, 0, fake, None, None) == 6
+    assert lib.xtq_vit_tailbite_dev_async(None, 4, 4, b"mul1", 0, 0, fake, None, None) == 12
     assert lib.xtq_vit_viterbi_dev(fake, 4, 300, 4, b"mul1", None, -1, fake, None) == 10
     assert lib.xtq_vit_viterbi_dev(fake, 4, 256, 4, b"mul1", None, 256, fake, None) == 10
     assert lib.xtq_trellis_decode_dev(fake, 1, 1, 8, b"mul1", fake, None, None) == 9

@@ -153,6 +153,45 @@ def test_nan_target_rejected(hb):
     assert st.shape == (2, 256)
 
 
+def test_async_encode_and_status(hb, oracle_mod, mul1_lut):
+    """Stream-ordered encodes equal the synchronous ones; a NaN target is
+    reported by the next status check (and only once)."""
+    rng = np.random.default_rng(11)
+    X = torch.from_numpy(rng.standard_normal((40, 256)).astype(np.float32)).cuda()
+    want, _ = hb.tailbite(X, 5, 147, 16)
+    outs = [hb.tailbite(X[i:i + 8], 5, 147, 16, sync=False)[0] for i in range(0, 40, 8)]
+    hb.status()
+    np.testing.assert_array_equal(torch.cat(outs).cpu().numpy(), want.cpu().numpy())
+    Xn = X.clone()
+    Xn[3, 200] = float("nan")
+    hb.tailbite(Xn, 5, 147, 16, sync=False)
+    with pytest.raises(hb.HipViterbiError) as ei:
+        hb.status()
+    assert ei.value.rc == 11
+    hb.status()                                      # flag cleared
+
+
+def test_async_two_streams_share_scratch(hb, oracle_mod, mul1_lut):
+    """Encodes issued on two streams without host waits in between (they
+    share the library's backpointer scratch) each match the oracle."""
+    rng = np.random.default_rng(12)
+    Xa = rng.standard_normal((300, 256)).astype(np.float32)
+    Xb = rng.standard_normal((700, 256)).astype(np.float32)
+    da, db = torch.from_numpy(Xa).cuda(), torch.from_numpy(Xb).cuda()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s1):
+        sa, _ = hb.tailbite(da, 4, 128, 0, sync=False)
+    with torch.cuda.stream(s2):
+        sb, _ = hb.tailbite(db, 4, 128, 0, sync=False)
+    torch.cuda.synchronize()
+    hb.status()
+    np.testing.assert_array_equal(sa.cpu().numpy(),
+                                  oracle_mod.tailbite(Xa, mul1_lut, 4, 16, pivot=128, margin=0))
+    np.testing.assert_array_equal(sb.cpu().numpy(),
+                                  oracle_mod.tailbite(Xb, mul1_lut, 4, 16, pivot=128, margin=0))
+
+
 def test_inf_targets_match_oracle(hb, oracle_mod, mul1_lut):
     """+-inf targets give all-inf costs; ties resolve like the reference."""
     X = np.random.default_rng(3).standard_normal((2, 256)).astype(np.float32)
