@@ -16,10 +16,15 @@ batch), targets resident in HBM before the timed region.  Prints one JSON line:
                bounded sample of the same tiles on this host's cores; the same
                sample (plus a larger one through the C oracle) gives bit_exact_pct
   k_sweep      tiles/s for K = 2..7 on the first 65,536 tiles
-  e2e          whole-tensor quantize_linear time (BlockLDLQ on the GPU) for a
-               4096x4096 weight with a synthetic AR(1) Hessian, K=4
+  configs      whole-tensor quantize_linear time with BlockLDLQ on the GPU for
+               the synthetic workloads c1..c5 (workloads.py; c3 for every K,
+               c4 the mixed-K qkv written as EXL3 tensors and checked with a
+               fused GEMV), each with its CPU baseline (the torch-CPU port on a
+               bounded sample of the first launch, extrapolated) and the first
+               two launches checked bit for bit against the C oracle
 
 Usage: python bench.py [--gpus 1] [--steps 3] [--warmup 1] [--no-extras]
+                       [--configs c1,c2,c3,c4,c5]
 """
 from __future__ import annotations
 
@@ -34,8 +39,10 @@ import torch
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "exl3xpu-mixedk_amd", "quantize"))
+import export_exl3 as ex  # noqa: E402
 import hip_backend as hb  # noqa: E402
 import quantize as xq  # noqa: E402
+import workloads as wl  # noqa: E402
 
 METRIC = "Viterbi tiles/sec (K=4, 256-wt tiles) on 1 MI355X; % VALU peak; bit-exact %"
 VALU_PEAK = 256 * 4 * 16 * 2.4e9          # 32-bit VALU lane-ops/s
@@ -54,9 +61,7 @@ def make_targets(seed: int = 4) -> torch.Tensor:
     fp16), random-sign + Hadamard incoherence, unit-rms scale, and the per-tile
     sequences x_t = tile[perm[t]] of every 16x16 tile -> [348160, 256] fp32."""
     dev = torch.device("cuda")
-    torch.manual_seed(seed)
-    t = torch.distributions.StudentT(torch.tensor(5.0, device=dev))
-    W = (t.sample((OUT_F, IN_F)) * (0.02 / (5.0 / 3.0) ** 0.5)).half().float()
+    W = wl.c5_weight(dev, seed=seed).float()                 # [5120 out, 17408 in]
     suh = xq.sign_vec(IN_F, 20261011, dev).half()
     svh = xq.sign_vec(OUT_F, 20261012, dev).half()
     h = xq.hadamard128(dev, torch.float32)
@@ -73,6 +78,17 @@ def make_targets(seed: int = 4) -> torch.Tensor:
 def run_step(X: torch.Tensor, K: int = KBITS):
     _, tr = hb.tailbite(X, K, PIVOT, MARGIN, states=False, trellis=True)
     return tr
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
 
 
 def cpu_baseline(X: torch.Tensor, trellis: torch.Tensor, budget_s: float = 12.0):
@@ -107,17 +123,8 @@ def cpu_baseline(X: torch.Tensor, trellis: torch.Tensor, budget_s: float = 12.0)
     want = O.tailbite(X[idx].cpu().numpy(), lut.numpy(), KBITS, 16, pivot=PIVOT,
                       margin=MARGIN, nthreads=cores)
     exact2 = int((want == gpu_states[idx].cpu().numpy()).all(axis=1).sum())
-    model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
     return ({"value": round(port_tps, 3), "unit": "tiles/s", "cores": cores, "kind": "port",
-             "cpu": model,
+             "cpu": _cpu_model(),
              "sample": f"{done} tiles drawn uniformly from the 348,160-tile K=4 workload, "
                        f"torch-CPU restatement of quantize_seq_tailbite, {cores} threads"},
             {"tiles_checked": done + len(idx), "tiles_exact": exact + exact2})
@@ -148,29 +155,164 @@ def k_sweep(X: torch.Tensor, n: int = 65536):
     return out
 
 
-def e2e_c2():
-    """quantize_linear on a 4096x4096 N(0, 0.02) weight with H = X^T X / 4096,
-    X rows AR(1) rho=0.5, BlockLDLQ on the GPU, K=4 (65,536 tiles)."""
-    dev = torch.device("cuda")
-    g = torch.Generator(device=dev).manual_seed(101)
-    d = 4096
-    Z = torch.randn(d, d, generator=g, device=dev, dtype=torch.float64)
-    Xh = torch.empty_like(Z)
-    Xh[:, 0] = Z[:, 0]
-    c = (1 - 0.25) ** 0.5
-    for i in range(1, d):
-        Xh[:, i] = 0.5 * Xh[:, i - 1] + c * Z[:, i]
-    H = (Xh.t() @ Xh / d).float()
-    del Z, Xh
-    W = (0.02 * torch.randn(d, d, generator=g, device=dev)).half().float()
-    torch.cuda.synchronize()
+class _LaunchCapture:
+    """Keeps device copies of the first `keep` BlockLDLQ launches (targets,
+    states) of a quantize_linear run, without host waits."""
+
+    def __init__(self, keep: int):
+        self.keep, self.kept, self.launches, self.real = keep, [], 0, None
+
+    def __enter__(self):
+        self.real = xq._launch
+
+        def hook(X, K, code, pivot, margin):
+            st, tr = self.real(X, K, code, pivot, margin)
+            if len(self.kept) < self.keep:
+                self.kept.append((X.clone(), st.clone(), K, pivot, margin))
+            self.launches += 1
+            return st, tr
+        xq._launch = hook
+        return self
+
+    def __exit__(self, *exc):
+        xq._launch = self.real
+
+
+def cpu_baseline_config(kept, total_tiles: int, port_tiles: int = 32):
+    """CPU leg of one config: the torch-CPU port of the reference Viterbi
+    timed on the first `port_tiles` tiles of the first launch (tiles/s,
+    extrapolated to the whole tensor), and every captured launch checked bit
+    for bit against the C oracle on the same targets."""
+    sys.path.insert(0, ROOT)
+    from oracle import oracle as O
+    from oracle import torch_port as TP
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    O.build()
+    lut = xq.get_lut("exl3_mul1")
+    X0, _, K, pivot, margin = kept[0]
+    xs = X0[:port_tiles].cpu()
     t0 = time.perf_counter()
-    r = xq.quantize_linear(W, H, K=4, device="cuda", margin=0)
+    TP.tailbite(xs.t().contiguous(), lut, K, 16, pivot=pivot, margin=margin)
+    tps = xs.shape[0] / (time.perf_counter() - t0)
+    checked = exact = 0
+    for X, st, K, pivot, margin in kept:
+        want = O.tailbite(X.cpu().numpy(), lut.numpy(), K, 16, pivot=pivot, margin=margin,
+                          nthreads=cores)
+        got = st.cpu().numpy()
+        checked += got.shape[0]
+        exact += int((got == want).all(axis=1).sum())
+    return ({"value": round(tps, 2), "unit": "tiles/s", "cores": cores, "kind": "port",
+             "cpu": _cpu_model(),
+             "sample": f"first {xs.shape[0]} tiles of the first BlockLDLQ launch",
+             "extrapolated_whole_tensor_s": round(total_tiles / tps, 1)},
+            {"launches_checked": len(kept), "tiles_checked": checked, "tiles_exact": exact})
+
+
+def _quantize_timed(W, H, K, cs, keep=2):
     torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
-    return {"workload": "4096x4096 N(0,0.02) fp16, AR(1) Hessian, BlockLDLQ on GPU, K=4",
-            "seconds": round(dt, 3), "tiles": 65536,
-            "proxy_loss": xq.hessian_weighted_err(W.cpu(), r["W_hat"], H.cpu())}
+    with _LaunchCapture(keep) as cap:
+        t0 = time.perf_counter()
+        r = xq.quantize_linear(W, H, K=K, device="cuda", margin=0, channel_scales=cs)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+    return r, dt, cap
+
+
+def _proxy_loss(W, W_hat, H) -> float:
+    """tr(dW H dW^T) / tr(W H W^T) (quantize.py:878-885), on the GPU."""
+    dW = W_hat.cuda() - W
+    return float(((dW @ H) * dW).sum() / ((W @ H) * W).sum())
+
+
+def _config_entry(W, H, K, cs, label):
+    r, dt, cap = _quantize_timed(W, H, K, cs)
+    tiles = W.numel() // 256
+    cb, chk = cpu_baseline_config(cap.kept, tiles)
+    e = {"workload": label, "K": K, "seconds": round(dt, 3), "tiles": tiles,
+         "tiles_per_s": round(tiles / dt, 1), "ldlq_launches": cap.launches,
+         "proxy_loss": _proxy_loss(W, r["W_hat"], H), "cpu_baseline": cb,
+         "bit_exact_pct": round(100.0 * chk["tiles_exact"] / max(1, chk["tiles_checked"]), 3),
+         "bit_exact_tiles": chk}
+    log(f"config {label}: {dt:.3f} s, {tiles / dt:,.0f} tiles/s, proxy {e['proxy_loss']:.3e}, "
+        f"bit-exact {e['bit_exact_pct']}% of {chk['tiles_checked']}")
+    return e, r
+
+
+def run_configs(names):
+    """Whole-tensor quantize_linear (BlockLDLQ on the GPU) for the synthetic
+    workloads; see workloads.py for the recipes."""
+    dev = torch.device("cuda")
+    out = {}
+    # library/solver warm-up outside the timed runs
+    Wt = torch.randn(256, 256, device=dev)
+    xq.quantize_linear(Wt, torch.eye(256, device=dev) + Wt.t() @ Wt / 256, K=4, device="cuda")
+    torch.cuda.synchronize()
+    if "c1" in names:
+        w = wl.c1()
+        out["c1"], _ = _config_entry(w["W"].float().to(dev), w["H"].to(dev), 4, False,
+                                     "c1 128x128 N(0,1), H=I, K=4")
+        # the whole config on the CPU port: 8 launches of 8 tiles
+        out["c1"]["note"] = "c1 is small enough that its CPU sample is half the tensor"
+    if "c2" in names:
+        w = wl.c2(device=dev)
+        out["c2"], _ = _config_entry(w["W"].float().to(dev), w["H"].to(dev), 4, False,
+                                     "c2 4096x4096 N(0,0.02), AR(1) rho=0.5, K=4")
+    if "c3" in names:
+        w = wl.c3(device=dev)
+        W, H = w["W"].float().to(dev), w["H"].to(dev)
+        out["c3"] = {}
+        for K in w["Ks"]:
+            out["c3"][f"K{K}"], _ = _config_entry(
+                W, H, K, False, f"c3 5120x5120 N(0,0.02)+0.1% 10-sigma outliers, AR(1) rho=0.5, K={K}")
+        del W, H
+    if "c4" in names:
+        w = wl.c4(device=dev)
+        H = w["H"].to(dev)
+        entry = {"workload": "c4 fused qkv: q 6144x5120 K=5, k/v 1024x5120 K=7, channel "
+                             "scales, EXL3 write + reconstruct + fused M=1 GEMV", "members": {}}
+        import tempfile
+        with tempfile.TemporaryDirectory() as td:
+            total, Ws = 0.0, []
+            for m in w["members"]:
+                Wm = m["W"].float().to(dev)
+                e, r = _config_entry(Wm, H, m["K"], True, f"c4 {m['module']} K={m['K']}")
+                entry["members"][m["module"]] = e
+                total += e["seconds"]
+                t0 = time.perf_counter()
+                ex.write_quantized(td, 0, m["module"], r)
+                entry["members"][m["module"]]["write_s"] = round(time.perf_counter() - t0, 3)
+            inputs = ex.collect_inputs(td)
+            for m in w["members"]:
+                base = f"model.language_model.layers.0.{m['module']}"
+                dt_, shp, raw = inputs[base + ".trellis"]
+                tr = torch.frombuffer(bytearray(raw), dtype=torch.int16).view(*shp)
+                suh = torch.frombuffer(bytearray(inputs[base + ".suh"][2]), dtype=torch.float16)
+                svh = torch.frombuffer(bytearray(inputs[base + ".svh"][2]), dtype=torch.float16)
+                Ws.append(ex.weight_orig(tr, suh, svh, m["K"], device=dev).t())
+        W_cat = torch.cat(Ws, 0)
+        x = w["x"].to(dev)
+        y16 = (x @ W_cat.half().t()).float()
+        y32 = x.float() @ W_cat.t()
+        entry["seconds"] = round(total, 3)
+        entry["gemv_rel_err_fp16_vs_fp32"] = float((y16 - y32).norm() / y32.norm())
+        W_orig = torch.cat([m["W"].float().to(dev) for m in w["members"]], 0)
+        y_o = x.float() @ W_orig.t()
+        entry["gemv_rel_err_vs_unquantized"] = float((y32 - y_o).norm() / y_o.norm())
+        out["c4"] = entry
+        log(f"config c4: {total:.3f} s, GEMV rel err {entry['gemv_rel_err_fp16_vs_fp32']:.2e}")
+        del H, W_cat
+    if "c5" in names:
+        w = wl.c5(device=dev)
+        W, H = w["W"].float().to(dev), w["H"].to(dev)
+        out["c5"] = {}
+        for K in w["Ks"]:
+            out["c5"][f"K{K}"], _ = _config_entry(
+                W, H, K, False, f"c5 5120x17408 Student-t(5) std 0.02, AR(1) rho=0.5 "
+                                f"(rank 4096) at d=17408, K={K}")
+        del W, H
+    torch.cuda.empty_cache()
+    return out
 
 
 def main():
@@ -179,7 +321,9 @@ def main():
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-extras", action="store_true",
-                    help="skip the CPU baseline, K sweep and end-to-end quantize")
+                    help="skip the CPU baseline, K sweep and the end-to-end configs")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5",
+                    help="comma-separated end-to-end workloads to run (empty: none)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="after the timed steps, copy a buffer of BYTES bytes three times "
                          "(a known-traffic kernel for scaling HBM counters)")
@@ -263,8 +407,12 @@ def main():
         result["bit_exact_tiles"] = chk
         log("k sweep ...")
         result["k_sweep"] = k_sweep(X)
-        log("end-to-end quantize 4096x4096 ...")
-        result["e2e"] = e2e_c2()
+        names = [c for c in args.configs.split(",") if c]
+        if names:
+            del X, tr
+            torch.cuda.empty_cache()
+            log(f"end-to-end configs {names} ...")
+            result["configs"] = run_configs(names)
     print(json.dumps(result), flush=True)
 
 

@@ -92,12 +92,13 @@ def c4(scale: int = 1, device="cpu") -> dict:
     return {"name": "c4", "members": members, "H": H, "x": x, "channel_scales": True}
 
 
-def c5_weight(device="cpu", scale: int = 1) -> torch.Tensor:
-    """Student-t(5) weight [5120 out, 17408 in] scaled to std 0.02 (fp16),
-    sampled on `device` under torch.manual_seed(4)."""
-    torch.manual_seed(4)
+def c5_weight(device="cpu", scale: int = 1, seed: int = 4) -> torch.Tensor:
+    """Student-t(5) weight [5120 out, 17408 in] scaled to std 0.02 (the
+    variance of Student-t(5) is 5/3), fp16, sampled on `device` under
+    torch.manual_seed(seed)."""
+    torch.manual_seed(seed)
     t = torch.distributions.StudentT(torch.tensor(5.0, device=device))
-    W = t.sample((_dim(5120, scale), _dim(17408, scale))) * (0.02 / math.sqrt(5.0 / 3.0))
+    W = t.sample((_dim(5120, scale), _dim(17408, scale))) * (0.02 / (5.0 / 3.0) ** 0.5)
     return W.half()
 
 
