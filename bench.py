@@ -11,7 +11,12 @@ batch), targets resident in HBM before the timed region.  Prints one JSON line:
                algorithmic lane-ops per launch (4 per trellis state per step:
                sub, mul, add, min) over its average launch time, measured with
                HIP events on the stream it runs on, against the MI355X VALU
-               peak 256 CU x 4 SIMD x 16 lanes x 2.4 GHz = 39.32e12 ops/s
+               peak 256 CU x 4 SIMD x 16 lanes x 2.4 GHz = 39.32e12 ops/s (one
+               wave64 VALU instruction per SIMD per 4 cycles).  gfx950 issues
+               adjacent independent v_mul_f32/v_add_f32 faster than that, so
+               roofline.mix_ceiling also gives the issue ceiling of the
+               kernel's own 4-instruction candidate mix, measured in the same
+               run by the library's VALU probe, and the kernel's share of it
   cpu_baseline the torch-CPU restatement of the reference Viterbi timed on a
                bounded sample of the same tiles on this host's cores; the same
                sample (plus a larger one through the C oracle) gives bit_exact_pct
@@ -379,6 +384,13 @@ def main():
                 "ops_per_launch": ops_per_launch,
                 "traceback_ms_per_step": round(prof["tb_ms"] / args.steps, 3),
                 "whole_job_frac": round(tps * OPS_PER_STATE_STEP * 65536 * 512 / VALU_PEAK, 4)}
+    probes = {name: hb.valu_probe(i) / 1e12 for i, name in enumerate(hb.VALU_PROBES)}
+    ceil = max(probes["candidate mix, dependency order"],
+               probes["candidate mix, grouped by opcode"])
+    roofline["mix_ceiling"] = {"value": round(ceil, 3), "unit": "TOP/s",
+                               "frac": round(achieved / ceil, 4),
+                               "probe_tlane_instr_per_s": {k: round(v, 2)
+                                                           for k, v in probes.items()}}
     tfile = os.path.join(ROOT, "profiles", "fwd_kernel_K4_traffic.json")
     if os.path.exists(tfile):
         with open(tfile) as f:

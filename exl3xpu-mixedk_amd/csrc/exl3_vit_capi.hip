@@ -89,7 +89,10 @@ struct DevCtx {
     size_t bp_cap = 0;
     int32_t* send = nullptr;
     int32_t* ov = nullptr;
+    uint32_t* flags = nullptr;   // fused tail-bite: pass-1 -> pass-2 ready flags
     size_t seq_cap = 0;
+    int32_t* counter = nullptr;  // fused tail-bite: task counter
+    uint32_t epoch = 0;          // fused tail-bite: value the current launch publishes
     float* hx = nullptr;       // staging for the host-pointer entries
     int32_t* hs = nullptr;
     size_t host_cap = 0;
@@ -176,6 +179,7 @@ int dev_init(int dev) {
     }
     if (hipMalloc((void**)&cx.err, sizeof(uint32_t)) != hipSuccess) return 2;
     if (hipMemset(cx.err, 0, sizeof(uint32_t)) != hipSuccess) return 1;
+    if (hipMalloc((void**)&cx.counter, sizeof(int32_t)) != hipSuccess) return 2;
     if (hipEventCreateWithFlags(&cx.last, hipEventDisableTiming) != hipSuccess) return 1;
     if (hipEventRecord(cx.last, 0) != hipSuccess) return 1;
     cx.owned = kNumCodes * 65536 * sizeof(uint16_t) + 256;
@@ -253,7 +257,7 @@ int reserve_scratch(DevCtx& cx, int K, int chunk) {
     // Device bytes this call adds to what the library already holds.
     size_t add = 0;
     if ((size_t)chunk * per > cx.bp_cap) add += (size_t)chunk * per - cx.bp_cap;
-    if ((size_t)chunk > cx.seq_cap) add += ((size_t)chunk - cx.seq_cap) * 2 * sizeof(int32_t);
+    if ((size_t)chunk > cx.seq_cap) add += ((size_t)chunk - cx.seq_cap) * 3 * sizeof(int32_t);
     if (cx.owned + add > g_maxbytes) {
         fprintf(stderr, "xtq_vit: request over XTQ_VIT_MAXBYTES (%zu)\n", g_maxbytes);
         return 5;
@@ -263,9 +267,12 @@ int reserve_scratch(DevCtx& cx, int K, int chunk) {
     cx.bp_cap = bpcap_bytes;
     size_t sc = cx.seq_cap;
     if ((size_t)chunk > sc) {
-        size_t sc2 = cx.seq_cap;
+        size_t sc2 = cx.seq_cap, sc3 = cx.seq_cap;
         if (grow(&cx.send, &sc, (size_t)chunk, sizeof(int32_t), &cx.owned)) return 2;
         if (grow(&cx.ov, &sc2, (size_t)chunk, sizeof(int32_t), &cx.owned)) return 2;
+        if (grow(&cx.flags, &sc3, (size_t)chunk, sizeof(uint32_t), &cx.owned)) return 2;
+        // fresh flags hold no epoch of a launch (epochs start at 1)
+        if (hipMemset(cx.flags, 0, (size_t)chunk * sizeof(uint32_t)) != hipSuccess) return 4;
         cx.seq_cap = sc;
     }
     return 0;
@@ -282,6 +289,11 @@ int finish(DevCtx& cx, hipStream_t s) {
     prof_collect();
     if (herr) {
         (void)hipMemset(cx.err, 0, sizeof(uint32_t));
+        if (herr & 6u) {
+            fprintf(stderr, "xtq_vit: fused tail-bite %s\n",
+                    (herr & 2u) ? "pass-2 wait expired" : "task out of range");
+            return 4;
+        }
         fprintf(stderr, "xtq_vit: NaN target\n");
         return 11;
     }
@@ -312,6 +324,21 @@ int scratch_end(DevCtx& cx, hipStream_t s, bool sync) {
     return sync ? finish(cx, s) : 0;
 }
 
+// Whether a chunk of n sequences runs as one fused two-pass launch:
+// XTQ_VIT_FUSED=0 never, =1 always, unset: batches below 4 sequences per CU
+// (where separate pass launches leave CUs idle in their last round).
+bool use_fused(const DevCtx& cx, int n) {
+    if (const char* e = getenv("XTQ_VIT_FUSED")) {
+        if (!strcmp(e, "0")) return false;
+        if (!strcmp(e, "1")) return true;
+    }
+    return n < 4 * (cx.ncu > 0 ? cx.ncu : 1);
+}
+
+// Polls before a pass-2 wait in the fused kernel gives up (~1 us each, so
+// seconds; a pass-1 task takes about a millisecond).
+constexpr int kSpinLimit = 1 << 22;
+
 // The two-pass tail-biting schedule over device buffers (quantize.py:323-354).
 int run_tailbite(DevCtx& cx, const float* dX, int nseq, int K, Code code, int margin,
                  int pivot, int32_t* d_states, int16_t* d_trellis, hipStream_t s,
@@ -327,6 +354,27 @@ int run_tailbite(DevCtx& cx, const float* dX, int nseq, int K, Code code, int ma
         const float* x = dX + (size_t)c0 * xtq::kSteps;
         const int T = pick_group(cx, K, n);
         hipError_t e;
+        if (use_fused(cx, n)) {
+            if (++cx.epoch == 0) cx.epoch = 1;
+            int pf = prof_begin(s, 0, (double)n * (n1 + xtq::kSteps));
+            e = xtq::launch_tailbite_fused(K, x, n, lut, pivot, n1, cx.bp, cx.send, cx.ov,
+                                           cx.flags, cx.counter, cx.epoch, kSpinLimit, cx.err,
+                                           s);
+            prof_end(pf, s);
+            if (e == hipSuccess) {
+                pf = prof_begin(s, 1, 0.0);
+                e = xtq::launch_traceback(
+                    K, cx.bp, n, cx.send, xtq::kSteps, 0, 0, nullptr,
+                    d_states ? d_states + (size_t)c0 * xtq::kSteps : nullptr,
+                    d_trellis ? d_trellis + (size_t)c0 * 16 * K : nullptr, s);
+                prof_end(pf, s);
+            }
+            if (e != hipSuccess) {
+                fprintf(stderr, "xtq_vit run: %s\n", hipGetErrorString(e));
+                return 4;
+            }
+            continue;
+        }
         // Pass 1: free run over the sequence rolled right by pivot, n1 steps,
         // traced back to step pivot: ov = s_pivot >> K.
         int pf = prof_begin(s, 0, (double)n * n1);

@@ -1,0 +1,154 @@
+// valu_probe.hip -- VALU issue-rate measurement for the forward DP's roofline.
+//
+// The forward DP spends one v_fma_mix_f32 (sub), v_mul_f32 (square),
+// v_add_f32 (add) and v_min_f64 (min/argmin) per trellis candidate.  On
+// gfx950 those instructions do not all issue at one wave64 instruction per
+// SIMD per 4 cycles: independent v_mul_f32 / v_add_f32 placed next to each
+// other issue faster.  These kernels time each instruction alone and the
+// four-instruction candidate mix (in dependency order and grouped by opcode)
+// on every CU, so the benchmark can report the kernel against the ceiling
+// its own instruction mix has on the GPU it runs on.
+//
+// Each thread runs kChains independent chains for kIters iterations and
+// writes one float; nothing else is read or written.
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+#include "../../include/exl3_vit.h"
+
+namespace {
+
+constexpr int kIters = 500;
+constexpr int kChains = 16;
+constexpr int kThreads = 1024;
+
+template <int OP>
+__global__ __launch_bounds__(kThreads) void probe_kernel(float* __restrict__ out, float b) {
+    float x[kChains];
+    double d[kChains];
+    uint32_t h[kChains];
+#pragma unroll
+    for (int c = 0; c < kChains; ++c) {
+        h[c] = 0x3c003c00u + threadIdx.x + c;      // fp16 pairs near 1.0
+        x[c] = 1.0f + 1e-3f * (float)(threadIdx.x + c);
+        d[c] = (double)x[c];
+    }
+    for (int it = 0; it < kIters; ++it) {
+        if constexpr (OP == 0) {
+#pragma unroll
+            for (int c = 0; c < kChains; ++c) asm volatile("v_mul_f32 %0, %0, %1" : "+v"(x[c]) : "v"(b));
+        } else if constexpr (OP == 1) {
+#pragma unroll
+            for (int c = 0; c < kChains; ++c) asm volatile("v_add_f32 %0, %0, %1" : "+v"(x[c]) : "v"(b));
+        } else if constexpr (OP == 2) {
+#pragma unroll
+            for (int c = 0; c < kChains; ++c)
+                asm volatile("v_fma_f32 %0, %0, %1, %1" : "+v"(x[c]) : "v"(b));
+        } else if constexpr (OP == 3) {
+#pragma unroll
+            for (int c = 0; c < kChains; ++c)
+                asm volatile("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]"
+                             : "=v"(x[c]) : "v"(h[c]), "v"(x[c]));
+        } else if constexpr (OP == 4) {
+#pragma unroll
+            for (int c = 0; c < kChains; ++c)
+                asm volatile("v_min_f64 %0, %0, %1" : "+v"(d[c]) : "v"((double)b));
+        } else if constexpr (OP == 5) {               // candidate mix, dependency order
+#pragma unroll
+            for (int c = 0; c < kChains; ++c) {
+                asm volatile("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]"
+                             : "=v"(x[c]) : "v"(h[c]), "v"(b));
+                asm volatile("v_mul_f32 %0, %0, %0" : "+v"(x[c]));
+                asm volatile("v_add_f32 %0, %0, %1" : "+v"(x[c]) : "v"(b));
+                asm volatile("v_min_f64 %0, %0, %1" : "+v"(d[c]) : "v"((double)b));
+            }
+        } else {                                     // candidate mix, grouped by 8
+#pragma unroll
+            for (int g0 = 0; g0 < kChains; g0 += 8) {
+#pragma unroll
+                for (int c = g0; c < g0 + 8; ++c)
+                    asm volatile("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]"
+                                 : "=v"(x[c]) : "v"(h[c]), "v"(b));
+#pragma unroll
+                for (int c = g0; c < g0 + 8; ++c) asm volatile("v_mul_f32 %0, %0, %0" : "+v"(x[c]));
+#pragma unroll
+                for (int c = g0; c < g0 + 8; ++c)
+                    asm volatile("v_add_f32 %0, %0, %1" : "+v"(x[c]) : "v"(b));
+#pragma unroll
+                for (int c = g0; c < g0 + 8; ++c)
+                    asm volatile("v_min_f64 %0, %0, %1" : "+v"(d[c]) : "v"((double)b));
+            }
+        }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kChains; ++c) s += x[c] + (float)d[c];
+    out[(size_t)blockIdx.x * kThreads + threadIdx.x] = s;
+}
+
+// VALU instructions per chain per iteration of each probe.
+constexpr int kOpsPerChain[7] = {1, 1, 1, 1, 1, 4, 4};
+
+template <int OP>
+hipError_t launch(int nwg, float* out, hipStream_t s) {
+    hipLaunchKernelGGL(probe_kernel<OP>, dim3(nwg), dim3(kThreads), 0, s, out, 1.0000001f);
+    return hipGetLastError();
+}
+
+hipError_t launch_any(int which, int nwg, float* out, hipStream_t s) {
+    switch (which) {
+        case 0: return launch<0>(nwg, out, s);
+        case 1: return launch<1>(nwg, out, s);
+        case 2: return launch<2>(nwg, out, s);
+        case 3: return launch<3>(nwg, out, s);
+        case 4: return launch<4>(nwg, out, s);
+        case 5: return launch<5>(nwg, out, s);
+        default: return launch<6>(nwg, out, s);
+    }
+}
+
+}  // namespace
+
+extern "C" int xtq_valu_probe(int which, double* lane_ops_per_s) {
+    if (!lane_ops_per_s) return 12;
+    if (which < 0 || which > 6) return 8;
+    int dev = 0, ncu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        ncu <= 0)
+        return 1;
+    const int nwg = 8 * ncu;
+    float* out = nullptr;
+    if (hipMalloc((void**)&out, (size_t)nwg * kThreads * sizeof(float)) != hipSuccess) return 2;
+    hipStream_t s = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    int rc = 0;
+    float best = 0.0f;
+    if (hipStreamCreate(&s) != hipSuccess || hipEventCreate(&e0) != hipSuccess ||
+        hipEventCreate(&e1) != hipSuccess) {
+        rc = 1;
+    } else if (launch_any(which, nwg, out, s) != hipSuccess ||
+               hipStreamSynchronize(s) != hipSuccess) {     // warm-up
+        rc = 4;
+    } else {
+        for (int r = 0; r < 3 && !rc; ++r) {
+            float ms = 0.0f;
+            if (hipEventRecord(e0, s) != hipSuccess || launch_any(which, nwg, out, s) != hipSuccess ||
+                hipEventRecord(e1, s) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+                hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
+                rc = 4;
+            else if (r == 0 || ms < best)
+                best = ms;
+        }
+    }
+    if (!rc) {
+        const double ops = (double)nwg * kThreads * kIters * kChains * kOpsPerChain[which];
+        *lane_ops_per_s = ops / (best * 1e-3);
+    }
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (s) (void)hipStreamDestroy(s);
+    (void)hipFree(out);
+    return rc;
+}

@@ -44,6 +44,20 @@ hipError_t launch_forward(int K, const float* X, int xstride, int xlen, int nseq
                           const int32_t* ov_in, void* bp, int32_t* send, uint32_t* err,
                           int group, hipStream_t stream);
 
+// Both tail-biting passes of nseq sequences (256-step targets X [nseq][256])
+// in one launch of 2*nseq workgroups (see tailbite_fused_kernel): pass 1
+// free on X rolled by pivot for n1 steps, traced back in-kernel to
+// ov = s_pivot >> K (ovbuf), pass 2 pinned to ov; send receives the pass-2
+// final states and bp the pass-2 backpointers (trace them back with
+// launch_traceback(K, bp, nseq, send, 256, 0, ...)).  flags [nseq] must hold
+// values != epoch on entry (epoch increases per launch; zero-filled memory
+// and epoch >= 1 work); counter is one device word.  err |= 2 when a pass-2
+// wait expires after spin_limit polls, |= 4 on a task outside the launch.
+hipError_t launch_tailbite_fused(int K, const float* X, int nseq, const uint16_t* lut16,
+                                 int pivot, int n1, void* bp, int32_t* send, int32_t* ovbuf,
+                                 uint32_t* flags, int32_t* counter, uint32_t epoch,
+                                 int spin_limit, uint32_t* err, hipStream_t stream);
+
 // Traceback of one run from send (the state at step nsteps-1) down to step
 // `stop`.  Writes sout[q] = s_stop >> shift (nullable), the nsteps states
 // (states [nseq][nsteps], nullable; needs stop == 0) and/or the packed EXL3

@@ -97,6 +97,17 @@ __device__ __forceinline__ double kmin_xor1(double k) {
     return kmin(k, key_of(plo, __uint_as_float(phi)));
 }
 
+// A global-memory pointer the caller knows to be the same in every lane,
+// moved to SGPRs and typed as global (so accesses through it are global_*
+// instructions, not flat ones, which would also count against lgkmcnt).
+typedef __attribute__((address_space(1))) uint8_t gbyte_t;
+__device__ __forceinline__ gbyte_t* uniform_gptr(uint8_t* p) {
+    const uint64_t v = (uint64_t)(size_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (gbyte_t*)(size_t)(((uint64_t)hi << 32) | lo);
+}
+
 // Byte address of a __shared__ location in the LDS aperture.
 __device__ __forceinline__ uint32_t lds_addr(const float* p) {
     return (uint32_t)(size_t)(__attribute__((address_space(3))) const float*)(p);
@@ -137,24 +148,36 @@ __device__ __forceinline__ int bp_lookup(const uint8_t* row, int j) {
 }
 
 // --------------------------------------------------------------- forward DP
-// One workgroup = 1024 threads = T sequences processed in lockstep (the
-// codebook registers are shared by the T sequences; one barrier per step).
+// Whether the candidate arithmetic is issued grouped by opcode (see fwd_run).
+template <int K>
+constexpr bool kGroupOps = (K >= 5);
+
+// Shared memory of one forward run over T sequences.
 template <int K, int T>
-__global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
-    const float* __restrict__ X, int xstride, int xlen, int nseq,
-    const uint16_t* __restrict__ lut16, int roll, int nsteps, int store_lo,
-    const int32_t* __restrict__ ov_in,
-    uint8_t* __restrict__ bp, int32_t* __restrict__ send, uint32_t* __restrict__ err,
-    float one) {
+struct FwdSmem {
+    __attribute__((aligned(16))) float bbuf[T][2][Geom<K>::SP];
+    float xs[T][kSteps];
+    int32_t ovs[T];                  // pin values (-1: free run), set by the caller
+    double red[kFwdThreads / 64];
+};
+
+// Forward DP of sequences q0 .. q0+ntile-1 (ntile <= T) in lockstep by one
+// 1024-thread workgroup (the codebook registers are shared by the T
+// sequences; one barrier per step).  The caller fills sm.ovs[0..T) before
+// the call; the final state of sequence q0+tt is written to send[tt] (global
+// or shared memory).
+template <int K, int T>
+__device__ __forceinline__ void fwd_run(
+    FwdSmem<K, T>& sm, const float* __restrict__ X, int xstride, int xlen, int q0, int ntile,
+    const uint16_t* __restrict__ lut16, int roll, int nsteps, int store_lo, bool pinned,
+    uint8_t* __restrict__ bp, int32_t* send, uint32_t* __restrict__ err, float one) {
     using G = Geom<K>;
-    __shared__ __attribute__((aligned(16))) float bbuf[T][2][G::SP];
-    __shared__ float xs[T][kSteps];
-    __shared__ int32_t ovs[T];
-    __shared__ double red[kFwdThreads / 64];
+    auto& bbuf = sm.bbuf;
+    auto& xs = sm.xs;
+    auto& ovs = sm.ovs;
+    auto& red = sm.red;
 
     const int tid = threadIdx.x;
-    const int q0 = blockIdx.x * T;
-    const int ntile = (nseq - q0) < T ? (nseq - q0) : T;   // sequences in this group
     if (tid < T * kSteps) {
         const int tt = tid / kSteps, e = tid % kSteps;
         float v = 0.0f;
@@ -164,9 +187,6 @@ __global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
         }
         xs[tt][e] = v;
     }
-    // Pinned runs (ov_in given) pin both ends to their ov; free runs use -1.
-    const bool pinned = (ov_in != nullptr);
-    if (tid < T) ovs[tid] = (pinned && tid < ntile) ? ov_in[q0 + tid] : -1;
 
     // Owned groups and candidates: groups j_c = jbase + c, candidate w of a
     // group is state j_c + (wbase + w) * SP; local index l = c*W + w.
@@ -237,13 +257,42 @@ __global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
                 for (int c = 0; c < G::C; ++c) {
                     const int blk = c / G::CB;
                     double kk[G::NCH];
+                    if constexpr (kGroupOps<K>) {
+                        // Issue the chunk's candidates opcode by opcode (all
+                        // subs, then all squares, then all adds): gfx950
+                        // issues adjacent independent v_mul_f32 / v_add_f32
+                        // faster than one per 4 cycles, which a
+                        // dependency-ordered schedule forfeits; the empty asm
+                        // statements fix the phase order.
+                        float dv[G::NCH];
 #pragma unroll
-                    for (int w = 0; w < G::NCH; ++w) {
-                        const int l = c * G::W + qc * G::NCH + w;
-                        const float fv = (l & 1) ? (float)fh[l >> 1].y : (float)fh[l >> 1].x;
-                        const float d = __builtin_fmaf(fv, one, negx);  // == fl(f - x)
-                        const float e = d * d;
-                        kk[w] = key_of(tag[w], e + B[blk][w]);
+                        for (int w = 0; w < G::NCH; ++w) {
+                            const int l = c * G::W + qc * G::NCH + w;
+                            const float fv =
+                                (l & 1) ? (float)fh[l >> 1].y : (float)fh[l >> 1].x;
+                            dv[w] = __builtin_fmaf(fv, one, negx);  // == fl(f - x)
+                        }
+#pragma unroll
+                        for (int w = 0; w < G::NCH; ++w) asm volatile("" : "+v"(dv[w]));
+#pragma unroll
+                        for (int w = 0; w < G::NCH; ++w) dv[w] = dv[w] * dv[w];
+#pragma unroll
+                        for (int w = 0; w < G::NCH; ++w) asm volatile("" : "+v"(dv[w]));
+#pragma unroll
+                        for (int w = 0; w < G::NCH; ++w)
+                            kk[w] = key_of(tag[w], dv[w] + B[blk][w]);
+                    } else {
+                        // K <= 4: the compiler's own interleaving measures
+                        // faster.
+#pragma unroll
+                        for (int w = 0; w < G::NCH; ++w) {
+                            const int l = c * G::W + qc * G::NCH + w;
+                            const float fv =
+                                (l & 1) ? (float)fh[l >> 1].y : (float)fh[l >> 1].x;
+                            const float d = __builtin_fmaf(fv, one, negx);  // == fl(f - x)
+                            const float e = d * d;
+                            kk[w] = key_of(tag[w], e + B[blk][w]);
+                        }
                     }
 #pragma unroll
                     for (int st = 1; st < G::NCH; st *= 2)
@@ -260,7 +309,11 @@ __global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
             }
             if constexpr (G::HALF) run[0] = kmin_xor1(run[0]);  // merge the two halves
 
-            uint8_t* bpq = bp + (size_t)q * ((size_t)kSlots * G::BPSTEP);
+            // this step's backpointer row: a wave-uniform base (SGPRs) plus a
+            // 32-bit lane offset, so the store takes the SGPR-base form and
+            // no 64-bit per-lane address is carried across steps
+            gbyte_t* const bprow =
+                uniform_gptr(bp + ((size_t)q * kSlots + (size_t)i) * G::BPSTEP);
             if (i + 1 < nsteps) {
                 float* bnext = bbuf[tt][(i + 1) & 1] + jbase;
                 if constexpr (G::C == 2 || G::C == 4) {
@@ -280,7 +333,7 @@ __global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
                 if (i >= store_lo) {
                     if constexpr (G::HALF) {
                         if ((tid & 1) == 0)
-                            bpq[(size_t)i * G::BPSTEP + jbase] = (uint8_t)(key_lo(run[0]) & 0x7F);
+                            bprow[(uint32_t)jbase] = (uint8_t)(key_lo(run[0]) & 0x7F);
                     } else {
                         // Funnel-shift each group's K index bits (the low bits
                         // of its key tag) in from the top, one v_alignbit_b32
@@ -291,7 +344,7 @@ __global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
                         for (int c = 0; c < G::C; ++c)
                             bits = __builtin_amdgcn_alignbit(key_lo(run[c]), bits, (uint32_t)K);
                         if constexpr (G::BITS < 32) bits >>= (32 - G::BITS);
-                        *(unit_t*)(bpq + (size_t)i * G::BPSTEP + (size_t)tid * G::UNIT) =
+                        *(__attribute__((address_space(1))) unit_t*)(bprow + (uint32_t)(tid * G::UNIT)) =
                             (unit_t)bits;
                     }
                 }
@@ -306,7 +359,7 @@ __global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
                 for (int c = 0; c < G::C; ++c)
                     if (jbase + c == ov && (!G::HALF || (tid & 1) == 0)) {
                         const float m = key_cost(run[c]);
-                        send[q] = (m == __builtin_inff())
+                        send[tt] = (m == __builtin_inff())
                                       ? 0
                                       : ov + (int)(key_lo(run[c]) & (uint32_t)(G::NC - 1)) * G::SP;
                     }
@@ -330,7 +383,7 @@ __global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
                     double b = red[0];
 #pragma unroll
                     for (int wv = 1; wv < kFwdThreads / 64; ++wv) b = kmin(b, red[wv]);
-                    send[q] = (int)key_lo(b);
+                    send[tt] = (int)key_lo(b);
                 }
                 __syncthreads();
             }
@@ -342,7 +395,61 @@ __global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
     }
 }
 
+// One workgroup advances sequences blockIdx.x*T .. +T-1; ov_in NULL = free
+// runs, else each run is pinned to its ov at both ends.
+template <int K, int T>
+__global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
+    const float* __restrict__ X, int xstride, int xlen, int nseq,
+    const uint16_t* __restrict__ lut16, int roll, int nsteps, int store_lo,
+    const int32_t* __restrict__ ov_in,
+    uint8_t* __restrict__ bp, int32_t* __restrict__ send, uint32_t* __restrict__ err,
+    float one) {
+    __shared__ FwdSmem<K, T> sm;
+    const int q0 = blockIdx.x * T;
+    const int ntile = (nseq - q0) < T ? (nseq - q0) : T;   // sequences in this group
+    const bool pinned = (ov_in != nullptr);
+    if (threadIdx.x < T)
+        sm.ovs[threadIdx.x] = (pinned && (int)threadIdx.x < ntile) ? ov_in[q0 + threadIdx.x] : -1;
+    fwd_run<K, T>(sm, X, xstride, xlen, q0, ntile, lut16, roll, nsteps, store_lo, pinned, bp,
+                  send + q0, err, one);
+}
+
 // ---------------------------------------------------------------- traceback
+// Traceback of one sequence by the calling workgroup: from cur = s_{nsteps-1}
+// (shared; set by the caller before a barrier) down to step `stop`.  The
+// backpointer slots stop .. nsteps-2 (slot i-1 links s_i to s_{i-1}) are
+// staged through `stage` in coalesced 16-byte loads by all threads, and one
+// thread chases the links in LDS.  On return (after a barrier) cur = s_stop
+// and st[i] = s_i for stop <= i <= nsteps-2 when st is non-null.
+template <int K>
+__device__ __forceinline__ void tb_chase(const uint8_t* __restrict__ bpq, int nsteps, int stop,
+                                         uint4* stage, int stage_bytes, int32_t* st,
+                                         int32_t& cur) {
+    using G = Geom<K>;
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const int ch = stage_bytes / G::BPSTEP;  // slots per staged chunk
+    for (int hi = nsteps - 2; hi >= stop; ) {
+        const int lo = (hi - ch + 1 > stop) ? hi - ch + 1 : stop;
+        const int n16 = (hi - lo + 1) * (G::BPSTEP / 16);
+        const uint4* src = (const uint4*)(bpq + (size_t)lo * G::BPSTEP);
+        __syncthreads();
+        for (int k = tid; k < n16; k += nthr) stage[k] = src[k];
+        __syncthreads();
+        if (tid == 0) {
+            int s = cur;
+            for (int sl = hi; sl >= lo; --sl) {
+                const int j = (s >> K) & (G::SP - 1);
+                const uint8_t* row = (const uint8_t*)stage + (size_t)(sl - lo) * G::BPSTEP;
+                s = j + bp_lookup<K>(row, j) * G::SP;
+                if (st) st[sl] = s;
+            }
+            cur = s;
+        }
+        hi = lo - 1;
+    }
+    __syncthreads();
+}
+
 template <int K>
 __global__ __launch_bounds__(kTbThreads) void tb_kernel(
     const uint8_t* __restrict__ bp, const int32_t* __restrict__ send, int nsteps, int stop,
@@ -350,7 +457,6 @@ __global__ __launch_bounds__(kTbThreads) void tb_kernel(
     int16_t* __restrict__ trellis) {
     using G = Geom<K>;
     constexpr int STAGE = 32768;
-    constexpr int CH = STAGE / G::BPSTEP;  // slots per staged chunk
     __shared__ uint4 stage[STAGE / 16];
     __shared__ int32_t st[kSteps];
     __shared__ int32_t cur;
@@ -362,27 +468,7 @@ __global__ __launch_bounds__(kTbThreads) void tb_kernel(
         cur = send[q] & 0xFFFF;
         if (keep) st[nsteps - 1] = cur;
     }
-    // Step i (s_i -> s_{i-1}) reads slot i-1; slots stop .. nsteps-2.
-    for (int hi = nsteps - 2; hi >= stop; ) {
-        const int lo = (hi - CH + 1 > stop) ? hi - CH + 1 : stop;
-        const int n16 = (hi - lo + 1) * (G::BPSTEP / 16);
-        const uint4* src = (const uint4*)(bpq + (size_t)lo * G::BPSTEP);
-        __syncthreads();
-        for (int k = tid; k < n16; k += kTbThreads) stage[k] = src[k];
-        __syncthreads();
-        if (tid == 0) {
-            int s = cur;
-            for (int sl = hi; sl >= lo; --sl) {
-                const int j = (s >> K) & (G::SP - 1);
-                const uint8_t* row = (const uint8_t*)stage + (size_t)(sl - lo) * G::BPSTEP;
-                s = j + bp_lookup<K>(row, j) * G::SP;
-                if (keep) st[sl] = s;
-            }
-            cur = s;
-        }
-        hi = lo - 1;
-    }
-    __syncthreads();
+    tb_chase<K>(bpq, nsteps, stop, stage, STAGE, keep ? st : nullptr, cur);
     if (sout && tid == 0) sout[q] = cur >> shift;
     if (states) {
         for (int t = tid; t < nsteps; t += kTbThreads) states[(size_t)q * nsteps + t] = st[t];
@@ -402,6 +488,84 @@ __global__ __launch_bounds__(kTbThreads) void tb_kernel(
         }
     }
 }
+
+// ------------------------------------------------------ fused tail-bite
+// Both QTIP passes of n sequences in one launch of 2n single-sequence
+// workgroups, for batches too small to fill the GPU twice over (the 16-row
+// blocks of the BlockLDLQ sweep: 64..384 tiles on 256 CUs).  Each workgroup
+// takes the next task from an atomic counter: tasks 0..n-1 run pass 1 (free
+// run of the rolled sequence, n1 steps) and trace it back inside the
+// workgroup to ov = s_pivot >> K, published with a release store of the
+// launch's epoch into flags[q]; tasks n..2n-1 wait for that flag (acquire)
+// and run pass 2 pinned to ov.  Tasks are taken in start order, so a pass-2
+// task only ever waits for a pass-1 task that is already running: the wait
+// always ends.  It is also bounded (spin_limit polls, err |= 2 on expiry)
+// so that an unexpected stall ends the launch with an error instead of a
+// hang.  With n = 320 on 256 CUs the 640 passes fill 3 rounds instead of the
+// 4 of two separate launches.  Pass-2 backpointers reuse the sequence's
+// pass-1 slots (pass 1 has finished reading them before it publishes); the
+// pass-2 traceback runs as tb_kernel afterwards.
+template <int K>
+__global__ __launch_bounds__(kFwdThreads) void tailbite_fused_kernel(
+    const float* __restrict__ X, int nseq, const uint16_t* __restrict__ lut16, int pivot,
+    int n1, uint8_t* __restrict__ bp, int32_t* __restrict__ send, int32_t* __restrict__ ovbuf,
+    uint32_t* __restrict__ flags, int32_t* __restrict__ counter, uint32_t epoch,
+    int spin_limit, uint32_t* __restrict__ err, float one) {
+    using G = Geom<K>;
+    __shared__ FwdSmem<K, 1> sm;
+    __shared__ int32_t task, cur;
+    const int tid = threadIdx.x;
+    if (tid == 0) task = atomicAdd(counter, 1);
+    __syncthreads();
+    const int t = task;
+    if (t >= 2 * nseq) {                       // cannot happen with a reset counter
+        if (tid == 0) atomicOr(err, 4u);
+        return;
+    }
+    if (t < nseq) {
+        if (tid == 0) sm.ovs[0] = -1;
+        fwd_run<K, 1>(sm, X, kSteps, kSteps, t, 1, lut16, pivot, n1, pivot, false, bp, &cur,
+                      err, one);
+        // This workgroup's backpointer stores reach L2 (and are written back
+        // past it, since pass 2 of this sequence may run on another XCD and
+        // overwrite them) before any thread reads them back.
+        __threadfence();
+        __syncthreads();
+        const uint8_t* bpq = bp + (size_t)t * ((size_t)kSlots * G::BPSTEP);
+        tb_chase<K>(bpq, n1, pivot, (uint4*)&sm.bbuf[0][0][0], (int)sizeof(sm.bbuf), nullptr,
+                    cur);
+        if (tid == 0) {
+            __hip_atomic_store(&ovbuf[t], cur >> K, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&flags[t], epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    } else {
+        const int q = t - nseq;
+        if (tid == 0) {
+            int ov = -1;
+            for (int it = 0;; ++it) {
+                if (__hip_atomic_load(&flags[q], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) ==
+                    epoch) {
+                    ov = __hip_atomic_load(&ovbuf[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                if (it >= spin_limit) {
+                    atomicOr(err, 2u);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(8);
+            }
+            sm.ovs[0] = ov;
+        }
+        __syncthreads();
+        if (sm.ovs[0] < 0) return;             // wait expired: reported through err
+        fwd_run<K, 1>(sm, X, kSteps, kSteps, q, 1, lut16, 0, kSteps, 0, true, bp, send + q,
+                      err, one);
+    }
+}
+
+// Resets the fused kernel's task counter (a kernel rather than a memset so
+// the sequence stays capturable in a HIP graph).
+__global__ void reset_counter_kernel(int32_t* counter) { *counter = 0; }
 
 // ------------------------------------------------- decode / pack / unpack
 // tensor_core_perm (quantize.py:101-118): element t -> row-major 16x16 index.
@@ -538,6 +702,20 @@ struct GroupSel {
 };
 
 template <int K>
+struct FusedL {
+    static hipError_t run(const float* X, int nseq, const uint16_t* lut16, int pivot, int n1,
+                          void* bp, int32_t* send, int32_t* ovbuf, uint32_t* flags,
+                          int32_t* counter, uint32_t epoch, int spin_limit, uint32_t* err,
+                          hipStream_t s) {
+        hipLaunchKernelGGL(reset_counter_kernel, dim3(1), dim3(1), 0, s, counter);
+        hipLaunchKernelGGL(tailbite_fused_kernel<K>, dim3(2 * nseq), dim3(kFwdThreads), 0, s,
+                           X, nseq, lut16, pivot, n1, (uint8_t*)bp, send, ovbuf, flags,
+                           counter, epoch, spin_limit, err, 1.0f);
+        return hipGetLastError();
+    }
+};
+
+template <int K>
 struct TbL {
     static hipError_t run(const void* bp, int nseq, const int32_t* send, int nsteps,
                           int stop, int shift, int32_t* sout, int32_t* states,
@@ -607,6 +785,17 @@ hipError_t launch_forward(int K, const float* X, int xstride, int xlen, int nseq
         return hipErrorInvalidValue;
     return dispatch_k<FwdL>(K, X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo, ov_in,
                             bp, send, err, group, stream);
+}
+
+hipError_t launch_tailbite_fused(int K, const float* X, int nseq, const uint16_t* lut16,
+                                 int pivot, int n1, void* bp, int32_t* send, int32_t* ovbuf,
+                                 uint32_t* flags, int32_t* counter, uint32_t epoch,
+                                 int spin_limit, uint32_t* err, hipStream_t stream) {
+    if (nseq <= 0) return hipSuccess;
+    if (pivot < 0 || pivot >= kSteps || n1 <= pivot || n1 > kSteps || spin_limit < 1)
+        return hipErrorInvalidValue;
+    return dispatch_k<FusedL>(K, X, nseq, lut16, pivot, n1, bp, send, ovbuf, flags, counter,
+                              epoch, spin_limit, err, stream);
 }
 
 hipError_t launch_traceback(int K, const void* bp, int nseq, const int32_t* send,

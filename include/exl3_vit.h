@@ -40,6 +40,9 @@
  *                    processed in chunks (default 8 GiB)
  *   XTQ_VIT_GROUP    force 1, 2 or 4 sequences per forward workgroup
  *                    (testing; default chosen from the batch size)
+ *   XTQ_VIT_FUSED    0: always run the two tail-biting passes as separate
+ *                    launches; 1: always as one fused launch (testing);
+ *                    default: fused for batches under 4 sequences per CU
  */
 #ifndef EXL3_VIT_H
 #define EXL3_VIT_H
@@ -165,6 +168,18 @@ int64_t xtq_vit_scratch_per_seq(int K);
 int xtq_vit_prof_enable(int on);
 int xtq_vit_prof_read(double* fwd_ms, int64_t* fwd_launches, double* fwd_seq_steps,
                       double* tb_ms, int64_t* tb_launches);
+
+/*
+ * VALU issue-rate probe (no reference counterpart; a measurement helper for
+ * the forward DP's roofline).  Times one probe kernel on every CU of the
+ * current device and returns its VALU lane-instructions per second:
+ *   0 v_mul_f32, 1 v_add_f32, 2 v_fma_f32, 3 v_fma_mix_f32, 4 v_min_f64,
+ *   5 the DP's candidate mix (v_fma_mix_f32, v_mul_f32, v_add_f32,
+ *     v_min_f64) in dependency order, 6 the same mix grouped by opcode.
+ * Returns 8 for an unknown probe, 2 if its small output buffer cannot be
+ * allocated, 4 on a HIP error.
+ */
+int xtq_valu_probe(int which, double* lane_ops_per_s);
 
 /* Static description of a status code. */
 const char* xtq_vit_strerror(int rc);

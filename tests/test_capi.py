@@ -72,6 +72,9 @@ def test_status_codes_without_device(lib):
     assert lib.xtq_vit_viterbi_dev(fake, 4, 256, 4, b"mul1", None, 256, fake, None) == 10
     assert lib.xtq_trellis_decode_dev(fake, 1, 1, 8, b"mul1", fake, None, None) == 9
     assert lib.xtq_trellis_pack_dev(fake, 1, 3, None, None) == 12
+    out = ctypes.c_double()
+    assert lib.xtq_valu_probe(7, ctypes.byref(out)) == 8
+    assert lib.xtq_valu_probe(0, None) == 12
     assert lib.xtq_vit_strerror(11) == b"NaN target"
     assert lib.xtq_vit_strerror(99) == b"unknown status"
 

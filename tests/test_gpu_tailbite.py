@@ -85,12 +85,17 @@ def test_short_runs_vs_oracle(hb, oracle_mod, mul1_lut, K):
 
 
 @pytest.mark.parametrize("K", range(2, 8))
-@pytest.mark.parametrize("group", ["1", "2", "4"])
+@pytest.mark.parametrize("group", ["1", "2", "4", "fused"])
 def test_oracle_random(hb, oracle_mod, mul1_lut, K, group, monkeypatch):
     """Random Gaussian and tie-heavy batches against the oracle, with each
-    sequences-per-workgroup code path forced, odd batch sizes included."""
-    monkeypatch.setenv("XTQ_VIT_GROUP", group)
-    rng = np.random.default_rng(1000 * K + int(group))
+    code path forced: separate pass launches at 1, 2 or 4 sequences per
+    workgroup, or the fused two-pass launch; odd batch sizes included."""
+    if group == "fused":
+        monkeypatch.setenv("XTQ_VIT_FUSED", "1")
+    else:
+        monkeypatch.setenv("XTQ_VIT_FUSED", "0")
+        monkeypatch.setenv("XTQ_VIT_GROUP", group)
+    rng = np.random.default_rng(1000 * K + (9 if group == "fused" else int(group)))
     n = 7
     X = rng.standard_normal((n, 256)).astype(np.float32)
     X[1] = mul1_lut[rng.integers(0, 65536, 256)]          # exact codebook values
@@ -103,6 +108,25 @@ def test_oracle_random(hb, oracle_mod, mul1_lut, K, group, monkeypatch):
         got, tr = _run(hb, X, K, pivot, margin, trellis=True)
         np.testing.assert_array_equal(got, want)
         np.testing.assert_array_equal(tr, oracle_mod.pack(want, K))
+
+
+@pytest.mark.parametrize("K,n", [(4, 320), (6, 320), (5, 384), (7, 64), (2, 257)])
+def test_fused_ldlq_sized_batches(hb, oracle_mod, mul1_lut, K, n, monkeypatch):
+    """Batch sizes of the BlockLDLQ sweep's launches (one 16-row block: tn
+    tiles), where the fused two-pass launch runs by default: identical to
+    the separate-launch path and to the oracle."""
+    rng = np.random.default_rng(300 + K)
+    X = rng.standard_normal((n, 256)).astype(np.float32)
+    X[::7] = mul1_lut[rng.integers(0, 65536, (len(X[::7]), 256))]
+    print(f"case fused K={K} n={n}", flush=True)
+    monkeypatch.delenv("XTQ_VIT_FUSED", raising=False)
+    fused, tr = _run(hb, X, K, 128, 0, trellis=True)
+    monkeypatch.setenv("XTQ_VIT_FUSED", "0")
+    split, _ = _run(hb, X, K, 128, 0)
+    np.testing.assert_array_equal(fused, split)
+    np.testing.assert_array_equal(fused, oracle_mod.tailbite(X, mul1_lut, K, 16, pivot=128,
+                                                             margin=0, nthreads=8))
+    np.testing.assert_array_equal(tr, oracle_mod.pack(fused, K))
 
 
 @pytest.mark.parametrize("K", (2, 4, 7))
@@ -151,6 +175,17 @@ def test_nan_target_rejected(hb):
     # the library recovers: a clean call afterwards succeeds
     st, _ = hb.tailbite(torch.randn(2, 256, device="cuda"), 4, 128, 0)
     assert st.shape == (2, 256)
+
+
+def test_valu_probe_rates(hb):
+    """The roofline probe runs and reports plausible rates: every probe
+    between 0.5x and 2.5x of one wave64 instruction per SIMD per 4 cycles."""
+    ncu = torch.cuda.get_device_properties(0).multi_processor_count
+    base = ncu * 64 * 2.4e9
+    for i, name in enumerate(hb.VALU_PROBES):
+        r = hb.valu_probe(i)
+        print(f"probe {name}: {r / 1e12:.2f} T/s", flush=True)
+        assert 0.5 * base < r < 2.5 * base, (name, r)
 
 
 def test_async_encode_and_status(hb, oracle_mod, mul1_lut):
