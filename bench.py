@@ -327,6 +327,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the CPU baseline, K sweep and the end-to-end configs")
+    ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-k-sweep", action="store_true", help="skip the K = 2..7 sweep")
     ap.add_argument("--configs", default="c1,c2,c3,c4,c5",
                     help="comma-separated end-to-end workloads to run (empty: none)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
@@ -412,13 +414,15 @@ def main():
               "ref_b70_tiles_per_s": REF_B70_TILES_PER_S,
               "speedup_vs_ref_b70": round(tps / REF_B70_TILES_PER_S, 1)}
     if not args.no_extras:
-        log("cpu baseline ...")
-        cb, chk = cpu_baseline(X, tr)
-        result["cpu_baseline"] = cb
-        result["bit_exact_pct"] = round(100.0 * chk["tiles_exact"] / chk["tiles_checked"], 3)
-        result["bit_exact_tiles"] = chk
-        log("k sweep ...")
-        result["k_sweep"] = k_sweep(X)
+        if not args.no_cpu_baseline:
+            log("cpu baseline ...")
+            cb, chk = cpu_baseline(X, tr)
+            result["cpu_baseline"] = cb
+            result["bit_exact_pct"] = round(100.0 * chk["tiles_exact"] / chk["tiles_checked"], 3)
+            result["bit_exact_tiles"] = chk
+        if not args.no_k_sweep:
+            log("k sweep ...")
+            result["k_sweep"] = k_sweep(X)
         names = [c for c in args.configs.split(",") if c]
         if names:
             del X, tr
