@@ -335,6 +335,16 @@ bool use_fused(const DevCtx& cx, int n) {
     return n < 4 * (cx.ncu > 0 ? cx.ncu : 1);
 }
 
+// Whether the tracebacks of a chunk of n sequences use one lane per
+// sequence: XTQ_VIT_TB_LANES=N sets the smallest such chunk (0: always,
+// -1: never); default 2048 (below it, whole-row staging by one workgroup per
+// sequence finishes sooner than a per-lane chain of dependent loads).
+bool use_lanes(int n) {
+    long long min_n = 2048;
+    if (const char* e = getenv("XTQ_VIT_TB_LANES")) min_n = atoll(e);
+    return min_n >= 0 && n >= min_n;
+}
+
 // Polls before a pass-2 wait in the fused kernel gives up (~1 us each, so
 // seconds; a pass-1 task takes about a millisecond).
 constexpr int kSpinLimit = 1 << 22;
@@ -366,7 +376,7 @@ int run_tailbite(DevCtx& cx, const float* dX, int nseq, int K, Code code, int ma
                 e = xtq::launch_traceback(
                     K, cx.bp, n, cx.send, xtq::kSteps, 0, 0, nullptr,
                     d_states ? d_states + (size_t)c0 * xtq::kSteps : nullptr,
-                    d_trellis ? d_trellis + (size_t)c0 * 16 * K : nullptr, s);
+                    d_trellis ? d_trellis + (size_t)c0 * 16 * K : nullptr, use_lanes(n), s);
                 prof_end(pf, s);
             }
             if (e != hipSuccess) {
@@ -384,7 +394,7 @@ int run_tailbite(DevCtx& cx, const float* dX, int nseq, int K, Code code, int ma
         if (e == hipSuccess) {
             pf = prof_begin(s, 1, 0.0);
             e = xtq::launch_traceback(K, cx.bp, n, cx.send, n1, pivot, K, cx.ov, nullptr,
-                                      nullptr, s);
+                                      nullptr, use_lanes(n), s);
             prof_end(pf, s);
         }
         // Pass 2: run pinned to ov on the unrolled sequence, full traceback.
@@ -399,7 +409,7 @@ int run_tailbite(DevCtx& cx, const float* dX, int nseq, int K, Code code, int ma
             e = xtq::launch_traceback(
                 K, cx.bp, n, cx.send, xtq::kSteps, 0, 0, nullptr,
                 d_states ? d_states + (size_t)c0 * xtq::kSteps : nullptr,
-                d_trellis ? d_trellis + (size_t)c0 * 16 * K : nullptr, s);
+                d_trellis ? d_trellis + (size_t)c0 * 16 * K : nullptr, use_lanes(n), s);
             prof_end(pf, s);
         }
         if (e != hipSuccess) {
@@ -429,10 +439,10 @@ int run_viterbi(DevCtx& cx, const float* dX, int nseq, int T, int K, Code code,
         if (e == hipSuccess) {
             if (back_from >= 0)
                 e = xtq::launch_traceback(K, cx.bp, n, cx.send, T, back_from, 0, d_out + c0,
-                                          nullptr, nullptr, s);
+                                          nullptr, nullptr, use_lanes(n), s);
             else
                 e = xtq::launch_traceback(K, cx.bp, n, cx.send, T, 0, 0, nullptr,
-                                          d_out + (size_t)c0 * T, nullptr, s);
+                                          d_out + (size_t)c0 * T, nullptr, use_lanes(n), s);
         }
         if (e != hipSuccess) {
             fprintf(stderr, "xtq_vit viterbi: %s\n", hipGetErrorString(e));

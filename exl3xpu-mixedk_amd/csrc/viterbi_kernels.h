@@ -62,10 +62,13 @@ hipError_t launch_tailbite_fused(int K, const float* X, int nseq, const uint16_t
 // `stop`.  Writes sout[q] = s_stop >> shift (nullable), the nsteps states
 // (states [nseq][nsteps], nullable; needs stop == 0) and/or the packed EXL3
 // trellis (trellis [nseq][16K] int16, nullable; needs stop == 0 and
-// nsteps == 256).
+// nsteps == 256).  lanes: one lane per sequence reading single backpointer
+// units (large batches) instead of one workgroup per sequence staging whole
+// rows through LDS (small batches).
 hipError_t launch_traceback(int K, const void* bp, int nseq, const int32_t* send,
                             int nsteps, int stop, int shift, int32_t* sout,
-                            int32_t* states, int16_t* trellis, hipStream_t stream);
+                            int32_t* states, int16_t* trellis, bool lanes,
+                            hipStream_t stream);
 
 // Trellis decode: int16 [tk][tn][16K] -> [16tk][16tn] (fp32 or fp16 bits).
 hipError_t launch_decode(int K, const int16_t* trellis, int tk, int tn,

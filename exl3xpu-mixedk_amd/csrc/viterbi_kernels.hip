@@ -450,6 +450,25 @@ __device__ __forceinline__ void tb_chase(const uint8_t* __restrict__ bpq, int ns
     __syncthreads();
 }
 
+// Word wd of one sequence's packed EXL3 trellis, from its states st[0..255]:
+// symbol t = s_t mod 2^K at stream bits [tK, (t+1)K), MSB first; 32-bit
+// words MSB first (quantize.py:360-378).
+template <int K, typename S>
+__device__ __forceinline__ uint32_t pack_word(const S* st, int wd) {
+    uint32_t word = 0;
+    for (int bb = 0; bb < 32; ++bb) {
+        const int b = wd * 32 + bb, t = b / K, k = b - t * K;
+        word |= (((uint32_t)st[t] >> (K - 1 - k)) & 1u) << (31 - bb);
+    }
+    return word;
+}
+
+// Stores a packed word as the int16 pair [low half, high half].
+__device__ __forceinline__ void store_word(int16_t* o, uint32_t word) {
+    o[0] = (int16_t)(uint16_t)(word & 0xFFFFu);
+    o[1] = (int16_t)(uint16_t)(word >> 16);
+}
+
 template <int K>
 __global__ __launch_bounds__(kTbThreads) void tb_kernel(
     const uint8_t* __restrict__ bp, const int32_t* __restrict__ send, int nsteps, int stop,
@@ -474,17 +493,54 @@ __global__ __launch_bounds__(kTbThreads) void tb_kernel(
         for (int t = tid; t < nsteps; t += kTbThreads) states[(size_t)q * nsteps + t] = st[t];
     }
     if (trellis && nsteps == kSteps) {
-        // Symbol t = s_t mod 2^K at stream bits [tK, (t+1)K), MSB first;
-        // 32-bit words MSB first, stored as int16 halves, low half first.
-        for (int wd = tid; wd < 8 * K; wd += kTbThreads) {
-            uint32_t word = 0;
-            for (int bb = 0; bb < 32; ++bb) {
-                const int b = wd * 32 + bb, t = b / K, k = b - t * K;
-                word |= (((uint32_t)st[t] >> (K - 1 - k)) & 1u) << (31 - bb);
-            }
-            int16_t* o = trellis + (size_t)q * 16 * K + 2 * wd;
-            o[0] = (int16_t)(uint16_t)(word & 0xFFFFu);
-            o[1] = (int16_t)(uint16_t)(word >> 16);
+        for (int wd = tid; wd < 8 * K; wd += kTbThreads)
+            store_word(trellis + (size_t)q * 16 * K + 2 * wd, pack_word<K>(st, wd));
+    }
+}
+
+// Traceback with one lane per sequence, for large batches: each lane chases
+// its sequence's links with dependent loads of just the backpointer unit
+// each step needs (1-4 bytes) instead of staging whole rows, so HBM reads
+// drop from 255 x BPSTEP bytes per sequence to one cache line per step; the
+// chase is latency-bound per sequence but all sequences chase at once.
+// States collect in LDS (odd dword row stride: conflict-free) and leave
+// coalesced, as states and/or the packed trellis.
+constexpr int kTbLaneSeqs = 64;
+
+template <int K>
+__global__ __launch_bounds__(kTbLaneSeqs) void tb_lane_kernel(
+    const uint8_t* __restrict__ bp, int nseq, const int32_t* __restrict__ send, int nsteps,
+    int stop, int shift, int32_t* __restrict__ sout, int32_t* __restrict__ states,
+    int16_t* __restrict__ trellis) {
+    using G = Geom<K>;
+    constexpr int ROW = kSteps + 2;
+    __shared__ uint16_t st[kTbLaneSeqs][ROW];
+    const int l = threadIdx.x;
+    const int q0 = blockIdx.x * kTbLaneSeqs;
+    const int q = q0 + l;
+    const bool keep = (states != nullptr) || (trellis != nullptr);
+    if (q < nseq) {
+        int s = send[q] & 0xFFFF;
+        if (keep) st[l][nsteps - 1] = (uint16_t)s;
+        const uint8_t* bpq = bp + (size_t)q * ((size_t)kSlots * G::BPSTEP);
+        for (int sl = nsteps - 2; sl >= stop; --sl) {
+            const int j = (s >> K) & (G::SP - 1);
+            s = j + bp_lookup<K>(bpq + (size_t)sl * G::BPSTEP, j) * G::SP;
+            if (keep) st[l][sl] = (uint16_t)s;
+        }
+        if (sout) sout[q] = s >> shift;
+    }
+    __syncthreads();
+    const int nt = (nseq - q0) < kTbLaneSeqs ? (nseq - q0) : kTbLaneSeqs;
+    if (states) {
+        for (int t = 0; t < nt; ++t)
+            for (int e = l; e < nsteps; e += kTbLaneSeqs)
+                states[(size_t)(q0 + t) * nsteps + e] = st[t][e];
+    }
+    if (trellis && nsteps == kSteps) {
+        for (int idx = l; idx < nt * 8 * K; idx += kTbLaneSeqs) {
+            const int t = idx / (8 * K), wd = idx - t * (8 * K);
+            store_word(trellis + (size_t)(q0 + t) * 16 * K + 2 * wd, pack_word<K>(st[t], wd));
         }
     }
 }
@@ -628,15 +684,8 @@ __global__ __launch_bounds__(64) void pack_kernel(const int32_t* __restrict__ st
                                                   int16_t* __restrict__ trellis) {
     const int tile = blockIdx.x, wd = threadIdx.x;
     if (wd >= 8 * K) return;
-    const int32_t* st = states + (size_t)tile * kSteps;
-    uint32_t word = 0;
-    for (int bb = 0; bb < 32; ++bb) {
-        const int b = wd * 32 + bb, t = b / K, k = b - t * K;
-        word |= (((uint32_t)st[t] >> (K - 1 - k)) & 1u) << (31 - bb);
-    }
-    int16_t* o = trellis + (size_t)tile * 16 * K + 2 * wd;
-    o[0] = (int16_t)(uint16_t)(word & 0xFFFFu);
-    o[1] = (int16_t)(uint16_t)(word >> 16);
+    store_word(trellis + (size_t)tile * 16 * K + 2 * wd,
+               pack_word<K>(states + (size_t)tile * kSteps, wd));
 }
 
 template <template <int> class F, typename... A>
@@ -719,10 +768,16 @@ template <int K>
 struct TbL {
     static hipError_t run(const void* bp, int nseq, const int32_t* send, int nsteps,
                           int stop, int shift, int32_t* sout, int32_t* states,
-                          int16_t* trellis, hipStream_t s) {
-        hipLaunchKernelGGL(tb_kernel<K>, dim3(nseq), dim3(kTbThreads), 0, s,
-                           (const uint8_t*)bp, send, nsteps, stop, shift, sout, states,
-                           trellis);
+                          int16_t* trellis, bool lanes, hipStream_t s) {
+        if (lanes)
+            hipLaunchKernelGGL(tb_lane_kernel<K>,
+                               dim3((nseq + kTbLaneSeqs - 1) / kTbLaneSeqs), dim3(kTbLaneSeqs),
+                               0, s, (const uint8_t*)bp, nseq, send, nsteps, stop, shift, sout,
+                               states, trellis);
+        else
+            hipLaunchKernelGGL(tb_kernel<K>, dim3(nseq), dim3(kTbThreads), 0, s,
+                               (const uint8_t*)bp, send, nsteps, stop, shift, sout, states,
+                               trellis);
         return hipGetLastError();
     }
 };
@@ -800,12 +855,12 @@ hipError_t launch_tailbite_fused(int K, const float* X, int nseq, const uint16_t
 
 hipError_t launch_traceback(int K, const void* bp, int nseq, const int32_t* send,
                             int nsteps, int stop, int shift, int32_t* sout, int32_t* states,
-                            int16_t* trellis, hipStream_t stream) {
+                            int16_t* trellis, bool lanes, hipStream_t stream) {
     if (nseq <= 0) return hipSuccess;
     if (nsteps < 1 || nsteps > kSteps || stop < 0 || stop >= nsteps)
         return hipErrorInvalidValue;
     return dispatch_k<TbL>(K, bp, nseq, send, nsteps, stop, shift, sout, states, trellis,
-                           stream);
+                           lanes, stream);
 }
 
 hipError_t launch_decode(int K, const int16_t* trellis, int tk, int tn, const uint16_t* lut16,

@@ -40,6 +40,8 @@
  *                    processed in chunks (default 8 GiB)
  *   XTQ_VIT_GROUP    force 1, 2 or 4 sequences per forward workgroup
  *                    (testing; default chosen from the batch size)
+ *   XTQ_VIT_TB_LANES smallest batch whose tracebacks run one lane per sequence
+ *                    (0: always, -1: never; default 2048)
  *   XTQ_VIT_FUSED    0: always run the two tail-biting passes as separate
  *                    launches; 1: always as one fused launch (testing);
  *                    default: fused for batches under 4 sequences per CU

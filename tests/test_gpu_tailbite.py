@@ -110,6 +110,31 @@ def test_oracle_random(hb, oracle_mod, mul1_lut, K, group, monkeypatch):
         np.testing.assert_array_equal(tr, oracle_mod.pack(want, K))
 
 
+@pytest.mark.parametrize("K", range(2, 8))
+def test_lane_traceback_vs_oracle(hb, oracle_mod, mul1_lut, K, monkeypatch):
+    """The one-lane-per-sequence traceback (forced at any batch size) equals
+    the oracle for tail-bites (both passes), full Viterbi runs and back_from,
+    with a partly filled last workgroup."""
+    monkeypatch.setenv("XTQ_VIT_FUSED", "0")
+    monkeypatch.setenv("XTQ_VIT_TB_LANES", "0")
+    rng = np.random.default_rng(700 + K)
+    n = 70
+    X = rng.standard_normal((n, 256)).astype(np.float32)
+    X[5] = mul1_lut[rng.integers(0, 65536, 256)]
+    X[6] = 0.0
+    for pivot, margin in ((128, 0), (147, 16), (3, 100)):
+        print(f"case lanes K={K} pivot={pivot} margin={margin}", flush=True)
+        got, tr = _run(hb, X, K, pivot, margin, trellis=True)
+        want = oracle_mod.tailbite(X, mul1_lut, K, 16, pivot=pivot, margin=margin)
+        np.testing.assert_array_equal(got, want)
+        np.testing.assert_array_equal(tr, oracle_mod.pack(want, K))
+    Xd = torch.from_numpy(X).cuda()
+    np.testing.assert_array_equal(hb.viterbi(Xd, K).cpu().numpy(),
+                                  oracle_mod.viterbi(X, mul1_lut, K, 16))
+    np.testing.assert_array_equal(hb.viterbi(Xd[:, :200].contiguous(), K, back_from=77).cpu().numpy(),
+                                  oracle_mod.viterbi(X[:, :200], mul1_lut, K, 16, back_from=77))
+
+
 @pytest.mark.parametrize("K,n", [(4, 320), (6, 320), (5, 384), (7, 64), (2, 257)])
 def test_fused_ldlq_sized_batches(hb, oracle_mod, mul1_lut, K, n, monkeypatch):
     """Batch sizes of the BlockLDLQ sweep's launches (one 16-row block: tn
