@@ -53,10 +53,21 @@ struct Geom {
     // Bytes per step: one unit per thread, or one byte per group when two
     // lanes share a group.
     static constexpr int BPSTEP = HALF ? SP : kFwdThreads * UNIT;
+    // LDS slots per b buffer.  With two lanes per group (K=7) the even and
+    // odd lanes of a wave read b at addresses 256 groups apart -- the same
+    // bank -- so group j lives at slot j + (j >> 8): one pad slot moves the
+    // upper half to the next bank (padded to keep rows 16-byte aligned).
+    static constexpr int SPL = HALF ? SP + 4 : SP;
     static_assert(NSTATE == 64, "64 states per thread");
     static_assert(BITS <= 32, "backpointer unit");
     static_assert(BPSTEP % 16 == 0, "staging granularity");
 };
+
+// LDS slot of group j in a b buffer (see Geom::SPL).
+template <int K>
+__device__ __forceinline__ int bslot(int j) {
+    return Geom<K>::HALF ? j + (j >> 8) : j;
+}
 
 template <int N> struct UnitT;
 template <> struct UnitT<1> { typedef uint8_t type; };
@@ -155,7 +166,7 @@ constexpr bool kGroupOps = (K >= 5);
 // Shared memory of one forward run over T sequences.
 template <int K, int T>
 struct FwdSmem {
-    __attribute__((aligned(16))) float bbuf[T][2][Geom<K>::SP];
+    __attribute__((aligned(16))) float bbuf[T][2][Geom<K>::SPL];
     float xs[T][kSteps];
     int32_t ovs[T];                  // pin values (-1: free run), set by the caller
     double red[kFwdThreads / 64];
@@ -217,13 +228,15 @@ __device__ __forceinline__ void fwd_run(
 #pragma unroll
             for (int c = 0; c < G::C; ++c) {
                 const int j = jbase + c;
-                bbuf[tt][0][j] = (ov < 0 || j == ov) ? 0.0f : __builtin_inff();
+                bbuf[tt][0][bslot<K>(j)] = (ov < 0 || j == ov) ? 0.0f : __builtin_inff();
             }
         }
     }
     __syncthreads();
 
     const int a0 = jbase >> K;  // first NC x NC block this thread reads
+    // b slot offset of every predecessor this lane reads (constant per lane)
+    const int rpad = bslot<K>(a0 + wbase * G::Q) - (a0 + wbase * G::Q);
     for (int i = 0; i < nsteps; ++i) {
         // Target of step i of the sequence rolled right by `roll`.
         const int u = (i - roll < 0) ? i - roll + xlen : i - roll;
@@ -245,7 +258,7 @@ __device__ __forceinline__ void fwd_run(
                 float B[G::NB][G::NCH];
 #pragma unroll
                 for (int w = 0; w < G::NCH; ++w) {
-                    const float* src = bcur + a0 + (wbase + qc * G::NCH + w) * G::Q;
+                    const float* src = bcur + a0 + rpad + (wbase + qc * G::NCH + w) * G::Q;
                     if constexpr (G::NB == 4) {
                         const float4 v = *(const float4*)src;
                         B[0][w] = v.x; B[1][w] = v.y; B[2][w] = v.z; B[3][w] = v.w;
@@ -315,7 +328,7 @@ __device__ __forceinline__ void fwd_run(
             gbyte_t* const bprow =
                 uniform_gptr(bp + ((size_t)q * kSlots + (size_t)i) * G::BPSTEP);
             if (i + 1 < nsteps) {
-                float* bnext = bbuf[tt][(i + 1) & 1] + jbase;
+                float* bnext = bbuf[tt][(i + 1) & 1] + bslot<K>(jbase);
                 if constexpr (G::C == 2 || G::C == 4) {
                     lds_store_costs<G::C>(lds_addr(bnext), run);
                 } else if constexpr (G::C % 4 == 0) {
@@ -705,7 +718,7 @@ hipError_t dispatch_k(int K, A... a) {
 // sequence) fits one CU's 160 KiB.
 template <int K>
 constexpr int max_group() {
-    constexpr size_t per = 2 * sizeof(float) * Geom<K>::SP + 1024 + 16;
+    constexpr size_t per = 2 * sizeof(float) * Geom<K>::SPL + 1024 + 16;
     return (4 * per + 512 <= 160 * 1024) ? 4 : (2 * per + 512 <= 160 * 1024) ? 2 : 1;
 }
 
