@@ -327,6 +327,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the CPU baseline, K sweep and the end-to-end configs")
+    ap.add_argument("--k", type=int, default=KBITS,
+                    help="bits per weight of the timed steps (profiling; the metric is K=4)")
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-k-sweep", action="store_true", help="skip the K = 2..7 sweep")
     ap.add_argument("--configs", default="c1,c2,c3,c4,c5",
@@ -348,8 +350,10 @@ def main():
     X = make_targets()
     n = X.shape[0]
     torch.cuda.synchronize()
+    if args.k != KBITS and not args.no_extras:
+        ap.error("--k other than 4 is a profiling option: use it with --no-extras")
     for w in range(args.warmup):
-        run_step(X)
+        run_step(X, args.k)
         torch.cuda.synchronize()
         log(f"warmup {w + 1}/{args.warmup} done")
     hb.prof_read()
@@ -357,7 +361,7 @@ def main():
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for s in range(args.steps):
-        tr = run_step(X)
+        tr = run_step(X, args.k)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     hb.prof_enable(False)
@@ -381,7 +385,7 @@ def main():
     roofline = {"bound": "valu", "achieved": round(achieved, 3), "peak": VALU_PEAK / 1e12,
                 "unit": "TOP/s", "frac": round(achieved / (VALU_PEAK / 1e12), 4),
                 "traffic": None,
-                "kernel": "fwd_kernel<4,4> (forward DP, both passes)",
+                "kernel": f"fwd_kernel<{args.k},T> (forward DP, both passes)",
                 "avg_launch_ms": round(fwd_avg_ms, 3),
                 "ops_per_launch": ops_per_launch,
                 "traceback_ms_per_step": round(prof["tb_ms"] / args.steps, 3),
@@ -408,7 +412,7 @@ def main():
               "config": {"workload": "17408x5120 fp16 weight at K=4: 348,160 independent "
                                      "16x16 tiles, tail-biting pivot 128 margin 0, packed "
                                      "EXL3 trellis out",
-                         "tiles": n, "K": KBITS, "pivot": PIVOT, "margin": MARGIN,
+                         "tiles": n, "K": args.k, "pivot": PIVOT, "margin": MARGIN,
                          "codebook": "exl3_mul1"},
               "roofline": roofline,
               "ref_b70_tiles_per_s": REF_B70_TILES_PER_S,
