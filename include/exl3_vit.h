@@ -51,6 +51,14 @@
 
 #include <stdint.h>
 
+/* The library is built with hidden symbol visibility; only these entry
+ * points are exported. */
+#if defined(__GNUC__) || defined(__clang__)
+#define XTQ_API __attribute__((visibility("default")))
+#else
+#define XTQ_API
+#endif
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -60,7 +68,7 @@ extern "C" {
  * quantize.py:497-503).  Selects the device (XTQ_VIT_DEVIDX) and uploads the
  * codebook tables.  Idempotent.
  */
-int xtq_vit_init(void);
+XTQ_API int xtq_vit_init(void);
 
 /*
  * Replaces quantize/viterbi_esimd.cpp:970 xtq_vit_run (bound by
@@ -70,7 +78,7 @@ int xtq_vit_init(void);
  *         three give identical results); "ih2x2" returns 8
  *   out   [nseq][256] int32 host: the pass-2 states
  */
-int xtq_vit_run(const float* X, int nseq, const char* code, int margin, int pivot,
+XTQ_API int xtq_vit_run(const float* X, int nseq, const char* code, int margin, int pivot,
                 int32_t* out);
 
 /*
@@ -78,7 +86,7 @@ int xtq_vit_run(const float* X, int nseq, const char* code, int margin, int pivo
  * reference kernel is K=4 only, viterbi_esimd.cpp:83,352; the torch path it
  * generalises is quantize.py:323-354).  code: "mul1", "3inst" or "mcg".
  */
-int xtq_vit_run_k(const float* X, int nseq, int K, const char* code, int margin,
+XTQ_API int xtq_vit_run_k(const float* X, int nseq, int K, const char* code, int margin,
                   int pivot, int32_t* out);
 
 /*
@@ -91,7 +99,7 @@ int xtq_vit_run_k(const float* X, int nseq, int K, const char* code, int margin,
  *   d_trellis [nseq][16K] int16 device (EXL3 trellis slices, pack_states
  *             layout quantize.py:360-378), or NULL
  */
-int xtq_vit_tailbite_dev(const float* dX, int nseq, int K, const char* code,
+XTQ_API int xtq_vit_tailbite_dev(const float* dX, int nseq, int K, const char* code,
                          int margin, int pivot, int32_t* d_states,
                          int16_t* d_trellis, void* stream);
 
@@ -105,7 +113,7 @@ int xtq_vit_tailbite_dev(const float* dX, int nseq, int K, const char* code,
  * Calls on different streams are ordered among themselves by the library
  * (they share its backpointer scratch).
  */
-int xtq_vit_tailbite_dev_async(const float* dX, int nseq, int K, const char* code,
+XTQ_API int xtq_vit_tailbite_dev_async(const float* dX, int nseq, int K, const char* code,
                                int margin, int pivot, int32_t* d_states,
                                int16_t* d_trellis, void* stream);
 
@@ -114,7 +122,7 @@ int xtq_vit_tailbite_dev_async(const float* dX, int nseq, int K, const char* cod
  * set since the last status or synchronous call: 0, or 11 (the flag is then
  * cleared), or 4 on a HIP error.
  */
-int xtq_vit_status_dev(void* stream);
+XTQ_API int xtq_vit_status_dev(void* stream);
 
 /*
  * Device-pointer single Viterbi run: the HIP counterpart of viterbi()
@@ -127,7 +135,7 @@ int xtq_vit_status_dev(void* stream);
  *              (links kept only after back_from, quantize.py:273-277,305-312)
  * Synchronous on return, like xtq_vit_tailbite_dev.
  */
-int xtq_vit_viterbi_dev(const float* dX, int nseq, int T, int K, const char* code,
+XTQ_API int xtq_vit_viterbi_dev(const float* dX, int nseq, int T, int K, const char* code,
                         const int32_t* d_overlap, int back_from, int32_t* d_out,
                         void* stream);
 
@@ -140,24 +148,24 @@ int xtq_vit_viterbi_dev(const float* dX, int nseq, int T, int K, const char* cod
  * Stream-ordered: returns once the kernel is enqueued on `stream` (as do
  * the pack and unpack entries below).
  */
-int xtq_trellis_decode_dev(const int16_t* d_trellis, int tk, int tn, int K,
+XTQ_API int xtq_trellis_decode_dev(const int16_t* d_trellis, int tk, int tn, int K,
                            const char* code, float* d_out_f32, uint16_t* d_out_f16,
                            void* stream);
 
 /* Device-pointer pack_states / unpack_states (quantize.py:360-402). */
-int xtq_trellis_pack_dev(const int32_t* d_states, int nt, int K, int16_t* d_trellis,
+XTQ_API int xtq_trellis_pack_dev(const int32_t* d_states, int nt, int K, int16_t* d_trellis,
                          void* stream);
-int xtq_trellis_unpack_dev(const int16_t* d_trellis, int nt, int K, int32_t* d_states,
+XTQ_API int xtq_trellis_unpack_dev(const int16_t* d_trellis, int nt, int K, int32_t* d_states,
                            void* stream);
 
 /*
  * Copies the fp32 decode table of `code` (65536 entries) into host memory
  * (the values get_lut returns, quantize.py:90-97).
  */
-int xtq_vit_get_lut(const char* code, float* out);
+XTQ_API int xtq_vit_get_lut(const char* code, float* out);
 
 /* Backpointer scratch bytes per sequence for K (sizing information). */
-int64_t xtq_vit_scratch_per_seq(int K);
+XTQ_API int64_t xtq_vit_scratch_per_seq(int K);
 
 /*
  * Kernel timing for benchmarks (no reference counterpart; the reference
@@ -167,8 +175,8 @@ int64_t xtq_vit_scratch_per_seq(int K);
  * forward milliseconds, forward launches, forward sequence-steps (sum of
  * sequences x steps over the launches), traceback milliseconds and launches.
  */
-int xtq_vit_prof_enable(int on);
-int xtq_vit_prof_read(double* fwd_ms, int64_t* fwd_launches, double* fwd_seq_steps,
+XTQ_API int xtq_vit_prof_enable(int on);
+XTQ_API int xtq_vit_prof_read(double* fwd_ms, int64_t* fwd_launches, double* fwd_seq_steps,
                       double* tb_ms, int64_t* tb_launches);
 
 /*
@@ -181,10 +189,10 @@ int xtq_vit_prof_read(double* fwd_ms, int64_t* fwd_launches, double* fwd_seq_ste
  * Returns 8 for an unknown probe, 2 if its small output buffer cannot be
  * allocated, 4 on a HIP error.
  */
-int xtq_valu_probe(int which, double* lane_ops_per_s);
+XTQ_API int xtq_valu_probe(int which, double* lane_ops_per_s);
 
 /* Static description of a status code. */
-const char* xtq_vit_strerror(int rc);
+XTQ_API const char* xtq_vit_strerror(int rc);
 
 #ifdef __cplusplus
 }
