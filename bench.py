@@ -161,8 +161,12 @@ def k_sweep(X: torch.Tensor, n: int = 65536):
 
 
 class _LaunchCapture:
-    """Keeps device copies of the first `keep` BlockLDLQ launches (targets,
-    states) of a quantize_linear run, without host waits."""
+    """Keeps device copies of a sample of a quantize_linear run's encodes
+    (targets, states, K, pivot, margin) for the bit-exact check, without host
+    waits.  Block schedule: the first `keep` BlockLDLQ launches.  Chain
+    schedule (one launch for the whole sweep): the kernel's own target dump,
+    sampled at `keep` block rows spread over the sweep (the first row swept,
+    which has no feedback, to the last, which has the most)."""
 
     def __init__(self, keep: int):
         self.keep, self.kept, self.launches, self.real = keep, [], 0, None
@@ -177,10 +181,23 @@ class _LaunchCapture:
             self.launches += 1
             return st, tr
         xq._launch = hook
+        xq.ldlq_viterbi.keep_targets = True
         return self
 
     def __exit__(self, *exc):
         xq._launch = self.real
+        xq.ldlq_viterbi.keep_targets = False
+        xt = xq.ldlq_viterbi.last_targets
+        if xt is not None and not self.kept:
+            tr = xq.ldlq_viterbi.last_trellis
+            tk, tn, K = tr.shape[0], tr.shape[1], tr.shape[2] // 16
+            st = hb.unpack(tr.reshape(-1, 16 * K), K).view(tk, tn, 256)
+            rows = sorted({tk - 1 - (r * (tk - 1)) // max(1, self.keep - 1)
+                           for r in range(self.keep)}, reverse=True)
+            for i in rows:
+                self.kept.append((xt[i].clone(), st[i].clone(), K, 128, 0))
+            self.launches = 1
+            xq.ldlq_viterbi.last_targets = None
 
 
 def cpu_baseline_config(kept, total_tiles: int, port_tiles: int = 32):
@@ -209,7 +226,7 @@ def cpu_baseline_config(kept, total_tiles: int, port_tiles: int = 32):
         exact += int((got == want).all(axis=1).sum())
     return ({"value": round(tps, 2), "unit": "tiles/s", "cores": cores, "kind": "port",
              "cpu": _cpu_model(),
-             "sample": f"first {xs.shape[0]} tiles of the first BlockLDLQ launch",
+             "sample": f"first {xs.shape[0]} tiles of the first 16-row block swept",
              "extrapolated_whole_tensor_s": round(total_tiles / tps, 1)},
             {"launches_checked": len(kept), "tiles_checked": checked, "tiles_exact": exact})
 

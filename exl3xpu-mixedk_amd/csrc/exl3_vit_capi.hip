@@ -93,6 +93,14 @@ struct DevCtx {
     size_t seq_cap = 0;
     int32_t* counter = nullptr;  // fused tail-bite: task counter
     uint32_t epoch = 0;          // fused tail-bite: value the current launch publishes
+    float* E = nullptr;          // column chains: (W - What)^T of finished tiles [n][k]
+    size_t e_cap = 0;            // floats
+    float* Lt = nullptr;         // column chains: transposed block-LDL factor [k][k]
+    size_t lt_cap = 0;           // floats
+    uint32_t* cflags = nullptr;  // column chains: tile-ready flags
+    size_t cflags_cap = 0;
+    float* xbuf = nullptr;       // column chains: each workgroup's target row
+    size_t xbuf_cap = 0;         // floats
     float* hx = nullptr;       // staging for the host-pointer entries
     int32_t* hs = nullptr;
     size_t host_cap = 0;
@@ -290,8 +298,8 @@ int finish(DevCtx& cx, hipStream_t s) {
     if (herr) {
         (void)hipMemset(cx.err, 0, sizeof(uint32_t));
         if (herr & 6u) {
-            fprintf(stderr, "xtq_vit: fused tail-bite %s\n",
-                    (herr & 2u) ? "pass-2 wait expired" : "task out of range");
+            fprintf(stderr, "xtq_vit: persistent kernel %s\n",
+                    (herr & 2u) ? "wait expired" : "task out of range");
             return 4;
         }
         fprintf(stderr, "xtq_vit: NaN target\n");
@@ -418,6 +426,52 @@ int run_tailbite(DevCtx& cx, const float* dX, int nseq, int K, Code code, int ma
         }
     }
     return scratch_end(cx, s, sync);
+}
+
+// The BlockLDLQ sweep as column chains in one persistent launch (see
+// ldlq_chain_kernel): library-owned E, tile flags, per-workgroup
+// backpointer slots and target rows.
+int run_ldlq_chain(DevCtx& cx, const float* W, const float* L, int k, int n, int K, Code code,
+                   int margin, int pivot, float* hatW, int32_t* states, int16_t* trellis,
+                   float* targets, hipStream_t s) {
+    const size_t ntile = (size_t)(k / 16) * (size_t)(n / 16);
+    const int nwg = cx.ncu > 0 ? cx.ncu : 1;     // one 1024-thread workgroup per CU
+    int rc = reserve_scratch(cx, K, nwg);
+    if (rc) return rc;
+    const size_t need_e = (size_t)k * n, need_x = targets ? 0 : (size_t)nwg * xtq::kSteps;
+    const size_t need_lt = L ? (size_t)k * k : 0;
+    size_t add = 0;
+    if (need_e > cx.e_cap) add += (need_e - cx.e_cap) * sizeof(float);
+    if (need_lt > cx.lt_cap) add += (need_lt - cx.lt_cap) * sizeof(float);
+    if (ntile > cx.cflags_cap) add += (ntile - cx.cflags_cap) * sizeof(uint32_t);
+    if (need_x > cx.xbuf_cap) add += (need_x - cx.xbuf_cap) * sizeof(float);
+    if (cx.owned + add > g_maxbytes) {
+        fprintf(stderr, "xtq_vit: request over XTQ_VIT_MAXBYTES (%zu)\n", g_maxbytes);
+        return 5;
+    }
+    if (add && hipEventSynchronize(cx.last) != hipSuccess) return 4;
+    if (grow(&cx.E, &cx.e_cap, need_e, sizeof(float), &cx.owned)) return 2;
+    if (grow(&cx.Lt, &cx.lt_cap, need_lt, sizeof(float), &cx.owned)) return 2;
+    if (ntile > cx.cflags_cap) {
+        if (grow(&cx.cflags, &cx.cflags_cap, ntile, sizeof(uint32_t), &cx.owned)) return 2;
+        if (hipMemset(cx.cflags, 0, ntile * sizeof(uint32_t)) != hipSuccess) return 4;
+    }
+    if (grow(&cx.xbuf, &cx.xbuf_cap, need_x, sizeof(float), &cx.owned)) return 2;
+    rc = scratch_begin(cx, s);
+    if (rc) return rc;
+    if (++cx.epoch == 0) cx.epoch = 1;
+    const int n1 = (margin > 0 && pivot + margin < xtq::kSteps) ? pivot + margin : xtq::kSteps;
+    const int pf = prof_begin(s, 0, (double)ntile * (n1 + xtq::kSteps));
+    const hipError_t e = xtq::launch_ldlq_chain(
+        K, W, L, cx.Lt, k, n, cx.lut16[code], pivot, n1, cx.bp, nwg, targets ? targets : cx.xbuf,
+        targets ? 1 : 0, hatW, cx.E, states, trellis, cx.cflags, cx.counter, cx.epoch,
+        kSpinLimit, cx.err, s);
+    prof_end(pf, s);
+    if (e != hipSuccess) {
+        fprintf(stderr, "xtq_vit ldlq chain: %s\n", hipGetErrorString(e));
+        return 4;
+    }
+    return scratch_end(cx, s, true);
 }
 
 // One Viterbi run (quantize.py:218-320) over device buffers: free or pinned,
@@ -593,6 +647,29 @@ int xtq_vit_status_dev(void* stream) {
     return finish(g_dev[dev], (hipStream_t)stream);
 }
 
+int xtq_ldlq_chain_dev(const float* d_W, const float* d_L, int k, int n, int K,
+                       const char* code, int margin, int pivot, float* d_hatW,
+                       int32_t* d_states, int16_t* d_trellis, float* d_targets, void* stream) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!d_W || !d_hatW || !d_trellis) return 12;
+    Code c;
+    int rc = parse_code(code, &c);
+    if (rc) return rc;
+    read_env();
+    if (K < 2 || K > 7) return 9;
+    if (pivot < 0 || pivot >= xtq::kSteps || margin < 0) return 10;
+    if (d_L && ((uintptr_t)d_L & 15)) return 12;     // rows are read as float4
+    if (k <= 0 || n <= 0 || k % 16 || n % 16 ||
+        (long long)(k / 16) * (n / 16) > g_maxseq || (long long)k * n > (1LL << 31) - 1)
+        return 6;
+    int dev = 0;
+    if (current_device(&dev)) return 1;
+    rc = dev_init(dev);
+    if (rc) return rc;
+    return run_ldlq_chain(g_dev[dev], d_W, d_L, k, n, K, c, margin, pivot, d_hatW, d_states,
+                          d_trellis, d_targets, (hipStream_t)stream);
+}
+
 int xtq_vit_viterbi_dev(const float* dX, int nseq, int T, int K, const char* code,
                         const int32_t* d_overlap, int back_from, int32_t* d_out,
                         void* stream) {
@@ -712,7 +789,7 @@ const char* xtq_vit_strerror(int rc) {
         case 9: return "unsupported K";
         case 10: return "pivot or margin out of range";
         case 11: return "NaN target";
-        case 12: return "null pointer argument";
+        case 12: return "null or misaligned pointer argument";
         default: return "unknown status";
     }
 }

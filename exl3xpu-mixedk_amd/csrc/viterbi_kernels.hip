@@ -176,19 +176,20 @@ struct FwdSmem {
 // 1024-thread workgroup (the codebook registers are shared by the T
 // sequences; one barrier per step).  The caller fills sm.ovs[0..T) before
 // the call; the final state of sequence q0+tt is written to send[tt] (global
-// or shared memory).
+// or shared memory).  tid is threadIdx.x (a persistent caller passes it
+// opaque per task, so that nothing derived from it is hoisted out of its
+// task loop and kept live across it).
 template <int K, int T>
 __device__ __forceinline__ void fwd_run(
     FwdSmem<K, T>& sm, const float* __restrict__ X, int xstride, int xlen, int q0, int ntile,
     const uint16_t* __restrict__ lut16, int roll, int nsteps, int store_lo, bool pinned,
-    uint8_t* __restrict__ bp, int32_t* send, uint32_t* __restrict__ err, float one) {
+    uint8_t* __restrict__ bp, int32_t* send, uint32_t* __restrict__ err, float one, int tid) {
     using G = Geom<K>;
     auto& bbuf = sm.bbuf;
     auto& xs = sm.xs;
     auto& ovs = sm.ovs;
     auto& red = sm.red;
 
-    const int tid = threadIdx.x;
     if (tid < T * kSteps) {
         const int tt = tid / kSteps, e = tid % kSteps;
         float v = 0.0f;
@@ -424,7 +425,7 @@ __global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
     if (threadIdx.x < T)
         sm.ovs[threadIdx.x] = (pinned && (int)threadIdx.x < ntile) ? ov_in[q0 + threadIdx.x] : -1;
     fwd_run<K, T>(sm, X, xstride, xlen, q0, ntile, lut16, roll, nsteps, store_lo, pinned, bp,
-                  send + q0, err, one);
+                  send + q0, err, one, (int)threadIdx.x);
 }
 
 // ---------------------------------------------------------------- traceback
@@ -594,7 +595,7 @@ __global__ __launch_bounds__(kFwdThreads) void tailbite_fused_kernel(
     if (t < nseq) {
         if (tid == 0) sm.ovs[0] = -1;
         fwd_run<K, 1>(sm, X, kSteps, kSteps, t, 1, lut16, pivot, n1, pivot, false, bp, &cur,
-                      err, one);
+                      err, one, tid);
         // This workgroup's backpointer stores reach L2 (and are written back
         // past it, since pass 2 of this sequence may run on another XCD and
         // overwrite them) before any thread reads them back.
@@ -628,7 +629,7 @@ __global__ __launch_bounds__(kFwdThreads) void tailbite_fused_kernel(
         __syncthreads();
         if (sm.ovs[0] < 0) return;             // wait expired: reported through err
         fwd_run<K, 1>(sm, X, kSteps, kSteps, q, 1, lut16, 0, kSteps, 0, true, bp, send + q,
-                      err, one);
+                      err, one, tid);
     }
 }
 
@@ -699,6 +700,233 @@ __global__ __launch_bounds__(64) void pack_kernel(const int32_t* __restrict__ st
     if (wd >= 8 * K) return;
     store_word(trellis + (size_t)tile * 16 * K + 2 * wd,
                pack_word<K>(states + (size_t)tile * kSteps, wd));
+}
+
+// ------------------------------------------------- BlockLDLQ column chains
+// The whole BlockLDLQ sweep (quantize.py:631-746) as one persistent launch.
+// The feedback of 16-row block i only mixes rows within an output column:
+// tile (i, j)'s targets are
+//     X[r][c] = W[16i+r][16j+c] + sum_{m >= 16(i+1)} L[m][16i+r] * E[m][16j+c],
+//     E = W - What  (the error of the tiles already quantized),
+// so tile (i, j) depends only on tile (i+1, j): the columns are independent
+// chains.  Each of the persistent workgroups takes tile tasks from an atomic
+// counter in sweep order (block tk-1 first), waits (acquire, bounded) for
+// the tile above in its column, computes the targets (the L and E columns
+// read as contiguous rows of their transposes Lt = L^T and Et = E^T, staged
+// through LDS), runs both tail-biting passes with in-workgroup tracebacks,
+// writes the states, the packed trellis, What and E for the tile, and
+// publishes the tile with a release store of the launch's epoch.  A task
+// only waits for a task taken before it, whose workgroup is running, so the
+// waits always end; columns advance independently, so the GPU is not left
+// half idle at the end of every block the way block-synchronous launches of
+// tn tiles are.  The feedback sums run in a fixed order of this kernel
+// (4 partial sums per element, one per quarter of each 128-row chunk, m
+// ascending, added pairwise at the end), not the reference's
+// lazily buffered GEMMs; the encode of each tile is bit-exact for the
+// targets it was given (xdump exposes them).
+constexpr int kChainRows = 128;    // L/E rows staged per feedback chunk
+constexpr int kChainDepth = 4;     // feedback chunks in flight per thread
+constexpr int kChainPad = kChainRows + 4;   // LDS row of a staged chunk
+
+// dst = src^T for a square [k][k] fp32 matrix, only the 64x64 tiles that
+// hold some element with row > column of src (the part the feedback reads).
+__global__ __launch_bounds__(256) void transpose_lower_kernel(const float* __restrict__ src,
+                                                              int k, float* __restrict__ dst) {
+    __shared__ float tile[64][65];
+    const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;   // src column / row block
+    if (r0 + 64 <= c0) return;                               // strictly above the diagonal
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    for (int yy = ty; yy < 64; yy += 4) {
+        const int r = r0 + yy, c = c0 + tx;
+        if (r < k && c < k) tile[yy][tx] = src[(size_t)r * k + c];
+    }
+    __syncthreads();
+    for (int yy = ty; yy < 64; yy += 4) {
+        const int r = c0 + yy, c = r0 + tx;                  // dst row = src column
+        if (r < k && c < k) dst[(size_t)r * k + c] = tile[tx][yy];
+    }
+}
+
+template <int K>
+__global__ __launch_bounds__(kFwdThreads) void ldlq_chain_kernel(
+    const float* __restrict__ W, const float* __restrict__ Lt, int k, int n,
+    const uint16_t* __restrict__ lut16, int pivot, int n1, uint8_t* __restrict__ bp,
+    float* __restrict__ xbuf, float* __restrict__ hatW, float* __restrict__ Et,
+    int32_t* __restrict__ states, int16_t* __restrict__ trellis, uint32_t* __restrict__ flags,
+    int32_t* __restrict__ counter, uint32_t epoch, int spin_limit, uint32_t* __restrict__ err,
+    int xdump, float one) {
+    using G = Geom<K>;
+    __shared__ FwdSmem<K, 1> sm;
+    // staged feedback chunk: lt[r][m] = L[m0+m][16i+r] = Lt[16i+r][m0+m],
+    // et[c][m] = E[m0+m][16j+c] = Et[16j+c][m0+m] (rows padded)
+    __shared__ __attribute__((aligned(16))) float lt[16][kChainPad];
+    __shared__ __attribute__((aligned(16))) float et[16][kChainPad];
+    __shared__ float part[4][256];
+    __shared__ int32_t st[kSteps];
+    __shared__ int32_t task, cur, ok;
+    const int tid = threadIdx.x;
+    const int tk = k / 16, tn = n / 16, ntask = tk * tn;
+    // this workgroup's backpointer slot and target row (or the dump row)
+    uint8_t* const bpw = bp + (size_t)blockIdx.x * ((size_t)kSlots * G::BPSTEP);
+    // Thread 0 publishes a finished tile and fetches the next task in ONE
+    // block right before the barrier that opens the loop body.  Two separate
+    // thread-0 blocks on either side of the back edge get merged by the
+    // compiler into a per-lane exit of the barrier loop: the other lanes of
+    // wave 0 then re-enter the body without thread 0 (stale task, no flag)
+    // and the launch never ends.  The loop-control values are read through
+    // readfirstlane so that the loop's exits are wave-uniform branches.
+    if (tid == 0) task = atomicAdd(counter, 1);
+    // A workgroup runs at most ntask tasks; the bound also ends the loop
+    // (err |= 4) should the task sequence ever fail to advance.
+    for (int done = 0;; ++done) {
+        __syncthreads();
+        const int t = __builtin_amdgcn_readfirstlane(task);
+        if (t >= ntask) break;
+        if (done >= ntask) {
+            if (tid == 0) atomicOr(err, 4u);
+            break;
+        }
+        const int i = tk - 1 - t / tn, j = t - (t / tn) * tn;
+        // targets row: the workgroup's own, or the tile's (row-block order)
+        float* const xs = xbuf + (xdump ? (size_t)i * tn + j : (size_t)blockIdx.x) * kSteps;
+        // wait for tile (i+1, j) (task t - tn)
+        if (tid == 0) {
+            int good = 1;
+            if (Lt != nullptr && i + 1 < tk) {
+                const uint32_t* f = flags + (size_t)(i + 1) * tn + j;
+                // relaxed polls (no cache invalidation per poll), one acquire
+                // fence once the flag is seen
+                for (int it = 0;; ++it) {
+                    if (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch) {
+                        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+                        break;
+                    }
+                    if (it >= spin_limit) {
+                        atomicOr(err, 2u);
+                        good = 0;
+                        break;
+                    }
+                    // another wait already expired: the chain will not
+                    // complete, so end this one too instead of timing out
+                    if ((it & 63) == 63 &&
+                        (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 2u)) {
+                        good = 0;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(8);
+                }
+            }
+            ok = good;
+        }
+        __syncthreads();
+        if (!__builtin_amdgcn_readfirstlane(ok)) break;
+        // targets: element e = 16r + c of the tile, 4 partial sums per element
+        {
+            const int e = tid & 255, pp = tid >> 8;
+            const int r = e >> 4, c = e & 15;
+            float acc = 0.0f;
+            if (Lt != nullptr && i + 1 < tk) {
+                // Chunks of kChainRows values m of the 16 rows Lt[16i+r]
+                // (threads 0..511) and Et[16j+c] (threads 512..1023): each
+                // row chunk is 512 contiguous bytes, one float4 per thread
+                // per chunk, kChainDepth chunks in flight.  Thread (e, pp)
+                // sums m = pp*32 .. pp*32+31 of every chunk, ascending.
+                const bool isl = tid < 512;
+                const int rr = (tid & 511) >> 5, q = tid & 31;
+                const float* src = isl ? Lt + (size_t)(16 * i + rr) * k + 4 * q
+                                       : Et + (size_t)(16 * j + rr) * k + 4 * q;
+                float* const dst = isl ? &lt[rr][4 * q] : &et[rr][4 * q];
+                const int mstart = 16 * (i + 1);
+                float4 pre[kChainDepth];
+#pragma unroll
+                for (int d = 0; d < kChainDepth; ++d) {
+                    const int mb = mstart + d * kChainRows;
+                    pre[d] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    if (mb + 4 * q < k) pre[d] = *(const float4*)(src + mb);
+                }
+                for (int m0 = mstart; m0 < k; m0 += kChainDepth * kChainRows) {
+#pragma unroll
+                    for (int d = 0; d < kChainDepth; ++d) {
+                        const int mb = m0 + d * kChainRows;
+                        if (mb < k) {
+                            __syncthreads();
+                            *(float4*)dst = pre[d];
+                            __syncthreads();
+                            const int mn = mb + kChainDepth * kChainRows;
+                            if (mn + 4 * q < k) pre[d] = *(const float4*)(src + mn);
+                            const int rows = (k - mb) < kChainRows ? (k - mb) : kChainRows;
+                            const int lo = pp * 32, hi = (lo + 32) < rows ? lo + 32 : rows;
+                            for (int mm = lo; mm < hi; mm += 4) {
+                                const float4 a = *(const float4*)&lt[r][mm];
+                                const float4 b = *(const float4*)&et[c][mm];
+                                acc = __builtin_fmaf(a.x, b.x, acc);
+                                acc = __builtin_fmaf(a.y, b.y, acc);
+                                acc = __builtin_fmaf(a.z, b.z, acc);
+                                acc = __builtin_fmaf(a.w, b.w, acc);
+                            }
+                        }
+                    }
+                }
+            }
+            part[pp][e] = acc;
+            __syncthreads();
+            if (tid < 256) {
+                const float fb = (part[0][tid] + part[1][tid]) + (part[2][tid] + part[3][tid]);
+                // sequence order: x_t = tile[perm[t]] (quantize.py:684-686)
+                const int pe = tid;                      // tile element handled here
+                const float x = W[(size_t)(16 * i + (pe >> 4)) * n + 16 * j + (pe & 15)] + fb;
+                part[0][pe] = x;
+            }
+            __syncthreads();
+            // thread q writes target q; fwd_run reads it back in thread q
+            if (tid < 256) xs[tid] = part[0][tc_perm(tid)];
+        }
+        __syncthreads();
+        // pass 1: free run of the sequence rolled by pivot, traced back to
+        // pivot; pass 2: pinned to ov = s_pivot >> K, full traceback into st
+        // (one call site of the forward body for both passes)
+#pragma unroll 1
+        for (int pass = 0; pass < 2; ++pass) {
+            const int nst = pass ? kSteps : n1, lo = pass ? 0 : pivot;
+            if (tid == 0) sm.ovs[0] = pass ? (cur >> K) : -1;
+            int tidv = tid;
+            const uint16_t* lutv = lut16;
+            asm volatile("" : "+v"(tidv));
+            asm volatile("" : "+s"(lutv));
+            fwd_run<K, 1>(sm, xs, kSteps, kSteps, 0, 1, lutv, pass ? 0 : pivot, nst, lo,
+                          pass != 0, bpw, &cur, err, one, tidv);
+            // the backpointers are read back by this workgroup only: the
+            // barrier's workgroup-scope ordering suffices
+            __syncthreads();
+            if (pass && tid == 0) st[kSteps - 1] = cur & 0xFFFF;
+            __syncthreads();
+            tb_chase<K>(bpw, nst, lo, (uint4*)&sm.bbuf[0][0][0], (int)sizeof(sm.bbuf),
+                        pass ? st : nullptr, cur);
+        }
+        // outputs of the tile
+        const size_t tile = (size_t)i * tn + j;
+        if (tid < kSteps) {
+            const int s = st[tid];
+            const int pe = tc_perm(tid);
+            const size_t g = (size_t)(16 * i + (pe >> 4)) * n + 16 * j + (pe & 15);
+            const float w = (float)__builtin_bit_cast(_Float16, lut16[s]);
+            hatW[g] = w;
+            Et[(size_t)(16 * j + (pe & 15)) * k + 16 * i + (pe >> 4)] = W[g] - w;
+            if (states) states[tile * kSteps + tid] = s;
+        } else if (tid < kSteps + 8 * K) {
+            const int wd = tid - kSteps;
+            store_word(trellis + tile * 16 * K + 2 * wd, pack_word<K>(st, wd));
+        }
+        // every wave's stores complete (explicitly: the barrier's
+        // workgroup-scope release does not wait for them) before thread 0's
+        // agent-scope release publishes them all with one L2 write-back
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tid == 0) {
+            __hip_atomic_store(flags + tile, epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+            task = atomicAdd(counter, 1);
+        }
+    }
 }
 
 template <template <int> class F, typename... A>
@@ -773,6 +1001,27 @@ struct FusedL {
         hipLaunchKernelGGL(tailbite_fused_kernel<K>, dim3(2 * nseq), dim3(kFwdThreads), 0, s,
                            X, nseq, lut16, pivot, n1, (uint8_t*)bp, send, ovbuf, flags,
                            counter, epoch, spin_limit, err, 1.0f);
+        return hipGetLastError();
+    }
+};
+
+template <int K>
+struct ChainL {
+    static hipError_t run(const float* W, const float* L, float* Lt, int k, int n,
+                          const uint16_t* lut16, int pivot, int n1, void* bp, int nwg,
+                          float* xbuf, int xdump, float* hatW, float* Et, int32_t* states,
+                          int16_t* trellis,
+                          uint32_t* flags, int32_t* counter, uint32_t epoch, int spin_limit,
+                          uint32_t* err, hipStream_t s) {
+        hipLaunchKernelGGL(reset_counter_kernel, dim3(1), dim3(1), 0, s, counter);
+        if (L != nullptr) {
+            const int nb = (k + 63) / 64;
+            hipLaunchKernelGGL(transpose_lower_kernel, dim3(nb, nb), dim3(256), 0, s, L, k, Lt);
+        }
+        hipLaunchKernelGGL(ldlq_chain_kernel<K>, dim3(nwg), dim3(kFwdThreads), 0, s, W,
+                           L != nullptr ? (const float*)Lt : nullptr, k, n, lut16, pivot, n1,
+                           (uint8_t*)bp, xbuf, hatW, Et, states, trellis, flags, counter, epoch,
+                           spin_limit, err, xdump, 1.0f);
         return hipGetLastError();
     }
 };
@@ -864,6 +1113,22 @@ hipError_t launch_tailbite_fused(int K, const float* X, int nseq, const uint16_t
         return hipErrorInvalidValue;
     return dispatch_k<FusedL>(K, X, nseq, lut16, pivot, n1, bp, send, ovbuf, flags, counter,
                               epoch, spin_limit, err, stream);
+}
+
+hipError_t launch_ldlq_chain(int K, const float* W, const float* L, float* Lt, int k, int n,
+                            const uint16_t* lut16, int pivot, int n1, void* bp, int nwg,
+                            float* xbuf, int xdump, float* hatW, float* Et, int32_t* states,
+                            int16_t* trellis, uint32_t* flags, int32_t* counter,
+                            uint32_t epoch, int spin_limit, uint32_t* err,
+                            hipStream_t stream) {
+    if (k <= 0 || n <= 0) return hipSuccess;
+    if (k % 16 || n % 16 || pivot < 0 || pivot >= kSteps || n1 <= pivot || n1 > kSteps ||
+        nwg < 1 || spin_limit < 1)
+        return hipErrorInvalidValue;
+    if (L != nullptr && Lt == nullptr) return hipErrorInvalidValue;
+    return dispatch_k<ChainL>(K, W, L, Lt, k, n, lut16, pivot, n1, bp, nwg, xbuf, xdump, hatW,
+                              Et, states, trellis, flags, counter, epoch, spin_limit, err,
+                              stream);
 }
 
 hipError_t launch_traceback(int K, const void* bp, int nseq, const int32_t* send,

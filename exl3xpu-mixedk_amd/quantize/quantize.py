@@ -40,6 +40,14 @@ sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
 import hip_backend as _hb  # noqa: E402
 
 BACKENDS = ("hip", "torch", "esimd")
+# BlockLDLQ schedules: "block" is the reference's sweep (one tail-bite launch
+# per 16-row block, feedback GEMMs in torch where W lives); "chain" runs the
+# whole sweep as tile column chains in one persistent GPU launch with the
+# feedback computed in the kernel; "auto" picks "chain" when W is on the GPU
+# and "block" otherwise (so CPU-side runs reproduce the reference's torch
+# arithmetic).
+SCHEDULES = ("auto", "block", "chain")
+DEFAULT_SCHEDULE = "auto"
 _DUAL_STATS: dict = {}
 
 
@@ -306,7 +314,8 @@ def ldlq_viterbi(Wq: torch.Tensor, Lfac: torch.Tensor | None, lut: torch.Tensor,
                  batch: int = 0, dtype: torch.dtype = torch.float32,
                  pivot: int | None = None, margin: int = 0,
                  compiled: bool = False, progress=None,
-                 code: str | None = None, backend: str = "hip"):
+                 code: str | None = None, backend: str = "hip",
+                 schedule: str | None = None):
     """BlockLDLQ trellis quantization of W_i [k, n] (quantize.py:631-746).
 
     Sweeps the 16-row blocks right to left.  Block i's targets are
@@ -316,9 +325,19 @@ def ldlq_viterbi(Wq: torch.Tensor, Lfac: torch.Tensor | None, lut: torch.Tensor,
     zeros gives plain Viterbi.  Returns (hatW [k, n] fp32, states int64
     [k/16, n/16, 256]) on Wq's device; the packed trellis of the sweep is left
     in ldlq_viterbi.last_trellis ([k/16, n/16, 16K] int16, GPU).
+
+    schedule (default DEFAULT_SCHEDULE) picks the sweep's launch schedule
+    (see SCHEDULES).  With "chain", ldlq_viterbi.keep_targets = True leaves
+    every tile's targets in ldlq_viterbi.last_targets ([k/16, n/16, 256]
+    fp32, sequence order, GPU).
     """
     if backend not in BACKENDS:
         raise ValueError(f"backend {backend!r} not in {BACKENDS}")
+    schedule = DEFAULT_SCHEDULE if schedule is None else schedule
+    if schedule not in SCHEDULES:
+        raise ValueError(f"schedule {schedule!r} not in {SCHEDULES}")
+    if schedule == "auto":
+        schedule = "chain" if Wq.is_cuda else "block"
     _check_viterbi_args(L, V, dtype, "sq")
     k, n = Wq.shape
     assert k % 16 == 0 and n % 16 == 0
@@ -328,8 +347,20 @@ def ldlq_viterbi(Wq: torch.Tensor, Lfac: torch.Tensor | None, lut: torch.Tensor,
     piv = 128 if pivot is None else int(pivot)
     perm = tensor_core_perm().to(dev)
     feedback = Lfac is not None and bool(Lfac.any())
-    Lf = Lfac.to(dev, Wq.dtype) if feedback else None
     tk, tn = k // 16, n // 16
+    ldlq_viterbi.last_targets = None
+    if schedule == "chain":
+        Wg = Wq.to(gdev, torch.float32).contiguous()
+        Lg = Lfac.to(gdev, torch.float32).contiguous() if feedback else None
+        hatW, states, trellis, xt = _hb.ldlq_chain(
+            Wg, Lg, K, piv, int(margin), code=kcode, states=True,
+            targets=bool(ldlq_viterbi.keep_targets))
+        if progress is not None:
+            progress(0, 512 * tk)
+        ldlq_viterbi.last_trellis = trellis
+        ldlq_viterbi.last_targets = xt
+        return hatW.to(dev), states.long().to(dev)
+    Lf = Lfac.to(dev, Wq.dtype) if feedback else None
 
     W_t = Wq.t().contiguous()                  # [n, k]
     hatW_t = torch.zeros_like(W_t)
@@ -367,6 +398,8 @@ def ldlq_viterbi(Wq: torch.Tensor, Lfac: torch.Tensor | None, lut: torch.Tensor,
 
 
 ldlq_viterbi.last_trellis = None
+ldlq_viterbi.last_targets = None
+ldlq_viterbi.keep_targets = False
 
 
 # ---------------------------------------------------------------- top level

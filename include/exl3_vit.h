@@ -125,6 +125,30 @@ XTQ_API int xtq_vit_tailbite_dev_async(const float* dX, int nseq, int K, const c
 XTQ_API int xtq_vit_status_dev(void* stream);
 
 /*
+ * The whole BlockLDLQ sweep (ldlq_viterbi, quantize.py:631-746) on the
+ * device, as column chains in one persistent launch: tile (i, j)'s targets
+ * are W[16i+r][16j+c] + sum_{m >= 16(i+1)} L[m][16i+r] (W - What)[m][16j+c],
+ * so each output column of tiles is an independent chain and the GPU is
+ * never idle at the end of a 16-row block.  No reference counterpart for
+ * the launch itself (the reference issues one tail-bite per 16-row block
+ * with torch GEMMs for the feedback); each tile's encode is bit-exact for
+ * its targets, which d_targets exposes.  The feedback sums are this
+ * kernel's own fixed-order fp32 dot products.  Synchronous on return.
+ *   d_W       [k][n] fp32 device, inner domain (k, n multiples of 16)
+ *   d_L       [k][k] fp32 device block-LDL factor (row-major, 16-byte
+ *             aligned), or NULL for no feedback
+ *   d_hatW    [k][n] fp32 device (out): the decoded tiles
+ *   d_states  [k/16 * n/16][256] int32 device (out), or NULL
+ *   d_trellis [k/16][n/16][16K] int16 device (out)
+ *   d_targets [k/16 * n/16][256] fp32 device (out: every tile's targets in
+ *             sequence order), or NULL
+ */
+XTQ_API int xtq_ldlq_chain_dev(const float* d_W, const float* d_L, int k, int n, int K,
+                               const char* code, int margin, int pivot, float* d_hatW,
+                               int32_t* d_states, int16_t* d_trellis, float* d_targets,
+                               void* stream);
+
+/*
  * Device-pointer single Viterbi run: the HIP counterpart of viterbi()
  * (quantize.py:218-320) with V = 1 and L = 16.
  *   dX         [nseq][T] fp32 device, 1 <= T <= 256

@@ -72,6 +72,16 @@ def test_status_codes_without_device(lib):
     assert lib.xtq_vit_viterbi_dev(fake, 4, 256, 4, b"mul1", None, 256, fake, None) == 10
     assert lib.xtq_trellis_decode_dev(fake, 1, 1, 8, b"mul1", fake, None, None) == 9
     assert lib.xtq_trellis_pack_dev(fake, 1, 3, None, None) == 12
+    ch = lib.xtq_ldlq_chain_dev
+    mis = ctypes.c_void_p(20)           # not 16-byte aligned
+    assert ch(fake, fake, 64, 64, 8, b"mul1", 0, 128, fake, None, fake, None, None) == 9
+    assert ch(fake, fake, 64, 64, 4, b"mul1", 0, 256, fake, None, fake, None, None) == 10
+    assert ch(fake, fake, 64, 64, 4, b"qtip", 0, 128, fake, None, fake, None, None) == 8
+    assert ch(None, fake, 64, 64, 4, b"mul1", 0, 128, fake, None, fake, None, None) == 12
+    assert ch(fake, fake, 64, 64, 4, b"mul1", 0, 128, fake, None, None, None, None) == 12
+    assert ch(fake, mis, 64, 64, 4, b"mul1", 0, 128, fake, None, fake, None, None) == 12
+    assert ch(fake, fake, 72, 64, 4, b"mul1", 0, 128, fake, None, fake, None, None) == 6
+    assert ch(fake, None, 64, 0, 4, b"mul1", 0, 128, fake, None, fake, None, None) == 6
     out = ctypes.c_double()
     assert lib.xtq_valu_probe(7, ctypes.byref(out)) == 8
     assert lib.xtq_valu_probe(0, None) == 12

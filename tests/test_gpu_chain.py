@@ -1,0 +1,183 @@
+"""GPU tests of the column-chain BlockLDLQ schedule (xtq_ldlq_chain_dev).
+
+The chain kernel computes every tile's targets itself, from the decoded
+tiles below it in its column, and encodes them.  The tests check
+  * every tile's targets against the BlockLDLQ target formula of
+    quantize.py:662-686 (X = W[block] + L[later, block]^T (W - What)[later])
+    evaluated in fp64 from the kernel's own What, within the rounding bound
+    of the kernel's fp32 sums -- a wrong index, sign or row range of the
+    feedback misses it by orders of magnitude;
+  * every tile's states bit for bit against the oracle on those targets, and
+    the packed trellis against the oracle's packing;
+  * decode(trellis) == What;
+  * whole-layer proxy loss against the reference's block schedule.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+U32 = 2.0 ** -24
+
+
+@pytest.fixture(scope="module")
+def xq():
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    import quantize
+    return quantize
+
+
+@pytest.fixture(scope="module")
+def hb():
+    import hip_backend
+    return hip_backend
+
+
+def _lfac(xq, k, seed, rho=0.5):
+    import workloads as wl
+    G = wl.ar1_gram(k, 2 * k, rho, seed).double()
+    G.diagonal().add_(0.01 * G.diagonal().mean())
+    L, _ = xq.block_LDL(G, 16)
+    return L.float()
+
+
+def _seq_order(T: torch.Tensor, perm: torch.Tensor) -> torch.Tensor:
+    """[k, n] -> [k/16, n/16, 256]: tile (i, j) in sequence order
+    x_t = tile[perm[t]] (quantize.py:684-686)."""
+    k, n = T.shape
+    tiles = T.reshape(k // 16, 16, n // 16, 16).permute(0, 2, 1, 3).reshape(k // 16, n // 16, 256)
+    return tiles[..., perm]
+
+
+def _check_targets(W, L, hatW, xt, perm):
+    """xt against the fp64 formula on the kernel's What.  The kernel sums each
+    target as 4 fp32 partial sums (one per quarter of every 128-row chunk, so
+    at most k/4 + 32 products each), adds the partials pairwise and then W:
+    its error is below (k/4 + 36) u times |W| + sum |L| |E| (u = 2^-24)."""
+    k, n = W.shape
+    W64 = W.double()
+    E = (W - hatW).double()              # the kernel's fp32 E, exactly
+    X64, B = W64.clone(), W64.abs()
+    if L is not None:
+        L64 = L.double()
+        for i in range(k // 16 - 1):
+            r0, r1 = 16 * i, 16 * (i + 1)
+            X64[r0:r1] += L64[r1:, r0:r1].t() @ E[r1:]
+            B[r0:r1] += L64[r1:, r0:r1].abs().t() @ E[r1:].abs()
+    d = (xt.double() - _seq_order(X64, perm)).abs()
+    lim = (k / 4 + 36) * U32 * _seq_order(B, perm)
+    assert (d <= lim).all(), f"worst excess {float((d - lim).max()):.3e}"
+    return float(d.max())
+
+
+def _check_tiles(oracle_mod, lut, K, pivot, margin, st, tr, xt, rows=None, cols=None):
+    """States of the selected tiles bit-exact with the oracle on the kernel's
+    own targets; trellis == oracle packing of those states."""
+    xs = xt if rows is None else xt[rows][:, cols]
+    ss = st if rows is None else st[rows][:, cols]
+    ts = tr if rows is None else tr[rows][:, cols]
+    want = oracle_mod.tailbite(xs.reshape(-1, 256).numpy(), lut, K, 16, pivot=pivot,
+                               margin=margin, nthreads=8)
+    np.testing.assert_array_equal(ss.reshape(-1, 256).numpy(), want)
+    np.testing.assert_array_equal(ts.reshape(-1, 16 * K).numpy(), oracle_mod.pack(want, K))
+
+
+@pytest.mark.parametrize("K,k,n,pivot,margin", [
+    (2, 128, 64, 128, 0), (3, 64, 96, 147, 16), (4, 128, 64, 128, 0),
+    (5, 96, 48, 5, 16), (6, 64, 64, 128, 0), (7, 128, 32, 250, 0)])
+def test_chain_vs_oracle(xq, hb, oracle_mod, mul1_lut, K, k, n, pivot, margin):
+    g = torch.Generator().manual_seed(40 + K)
+    W = torch.randn(k, n, generator=g)
+    L = _lfac(xq, k, K)
+    print(f"case chain K={K} {k}x{n} pivot={pivot} margin={margin}", flush=True)
+    hatW, st, tr, xt = hb.ldlq_chain(W.cuda(), L.cuda(), K, pivot, margin, targets=True)
+    hatW, st, tr, xt = (t.cpu() for t in (hatW, st, tr, xt))
+    perm = xq.tensor_core_perm()
+    _check_targets(W, L, hatW, xt, perm)
+    _check_tiles(oracle_mod, mul1_lut, K, pivot, margin, st, tr, xt)
+    np.testing.assert_array_equal(hatW.numpy(), oracle_mod.decode(tr.numpy(), mul1_lut, K))
+
+
+def test_chain_without_feedback(xq, hb, oracle_mod, mul1_lut):
+    """L = None: every tile's targets are its own W values, and the encode is
+    the plain tail-bite of each tile."""
+    g = torch.Generator().manual_seed(7)
+    W = torch.randn(64, 128, generator=g)
+    print("case chain K=4 64x128 no feedback", flush=True)
+    hatW, st, tr, xt = (t.cpu() for t in hb.ldlq_chain(W.cuda(), None, 4, 128, 0, targets=True))
+    assert torch.equal(xt, _seq_order(W, xq.tensor_core_perm()))
+    _check_tiles(oracle_mod, mul1_lut, 4, 128, 0, st, tr, xt)
+    np.testing.assert_array_equal(hatW.numpy(), oracle_mod.decode(tr.numpy(), mul1_lut, 4))
+
+
+def test_chain_one_long_column(xq, hb, oracle_mod, mul1_lut):
+    """n = 16: a single chain of 32 tiles, each waiting for the one before."""
+    g = torch.Generator().manual_seed(8)
+    W = torch.randn(512, 16, generator=g)
+    L = _lfac(xq, 512, 8, rho=0.8)
+    print("case chain K=3 512x16 single column", flush=True)
+    hatW, st, tr, xt = (t.cpu() for t in hb.ldlq_chain(W.cuda(), L.cuda(), 3, 128, 0,
+                                                        targets=True))
+    _check_targets(W, L, hatW, xt, xq.tensor_core_perm())
+    _check_tiles(oracle_mod, mul1_lut, 3, 128, 0, st, tr, xt)
+
+
+def test_chain_many_tasks_per_workgroup(xq, hb, oracle_mod, mul1_lut):
+    """2048 tiles: several tasks per persistent workgroup; targets of every
+    tile checked, states of the first and last block rows at both edges."""
+    g = torch.Generator().manual_seed(9)
+    W = torch.randn(256, 2048, generator=g)
+    L = _lfac(xq, 256, 9)
+    print("case chain K=4 256x2048", flush=True)
+    hatW, st, tr, xt = (t.cpu() for t in hb.ldlq_chain(W.cuda(), L.cuda(), 4, 128, 0,
+                                                        targets=True))
+    _check_targets(W, L, hatW, xt, xq.tensor_core_perm())
+    cols = list(range(8)) + list(range(120, 128))
+    _check_tiles(oracle_mod, mul1_lut, 4, 128, 0, st, tr, xt, rows=[0, 15], cols=cols)
+    np.testing.assert_array_equal(hatW.numpy(), oracle_mod.decode(tr.numpy(), mul1_lut, 4))
+
+
+def test_chain_outputs_without_dump(hb):
+    """Without the targets dump (per-workgroup target rows) the outputs are
+    the same, and repeated launches (epochs) agree."""
+    g = torch.Generator().manual_seed(10)
+    W = torch.randn(128, 512, generator=g).cuda()
+    L = torch.tril(0.05 * torch.randn(128, 128, generator=g), -16).cuda().contiguous()
+    a = hb.ldlq_chain(W, L, 5, 128, 0, targets=True)
+    for _ in range(2):
+        b = hb.ldlq_chain(W, L, 5, 128, 0, targets=False)
+        assert b[3] is None
+        for x, y in zip(a[:3], b[:3]):
+            assert torch.equal(x, y)
+
+
+def test_chain_nan_rejected(hb):
+    W = torch.randn(64, 64, device="cuda")
+    W[40, 3] = float("nan")
+    L = torch.tril(0.1 * torch.ones(64, 64), -16).cuda().contiguous()
+    with pytest.raises(hb.HipViterbiError) as ei:
+        hb.ldlq_chain(W, L, 4, 128, 0)
+    assert ei.value.rc == 11
+    hatW, *_ = hb.ldlq_chain(torch.randn(64, 64, device="cuda"), L, 4, 128, 0)
+    assert torch.isfinite(hatW).all()
+
+
+def test_chain_vs_block_schedule(xq, monkeypatch):
+    """quantize_linear with the sweep as column chains and as the reference's
+    block schedule: the same encoder on targets that differ only in fp32
+    rounding of the feedback, so the proxy losses agree closely."""
+    import workloads as wl
+    g = torch.Generator().manual_seed(11)
+    W = 0.02 * torch.randn(256, 512, generator=g)
+    H = wl.ar1_gram(512, 1024, 0.5, 11)
+    res = {}
+    for sched in ("chain", "block"):
+        monkeypatch.setattr(xq, "DEFAULT_SCHEDULE", sched)
+        print(f"case quantize_linear 256x512 schedule={sched}", flush=True)
+        r = xq.quantize_linear(W, H, K=4, device="cuda", margin=0)
+        res[sched] = (r, xq.hessian_weighted_err(W, r["W_hat"], H))
+    e_c, e_b = res["chain"][1], res["block"][1]
+    same = (res["chain"][0]["trellis"] == res["block"][0]["trellis"]).all(dim=-1).float().mean()
+    print(f"proxy chain {e_c:.6e} block {e_b:.6e}, identical tiles {float(same):.3f}")
+    assert abs(e_c - e_b) <= 0.01 * e_b

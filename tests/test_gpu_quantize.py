@@ -116,6 +116,7 @@ def test_dual_ldlq_on_gpu(xq, oracle_mod, mul1_lut, monkeypatch):
     H = _ar1_hessian(256, 512, 0.5, 1)
     stats = {"launches": 0, "tiles": 0, "mismatch_tiles": 0}
     real = xq._launch
+    monkeypatch.setattr(xq, "DEFAULT_SCHEDULE", "block")   # one launch per 16-row block
 
     def dual(X, K, code, pivot, margin):
         st, tr = real(X, K, code, pivot, margin)
