@@ -231,14 +231,16 @@ def cpu_baseline_config(kept, total_tiles: int, port_tiles: int = 32):
             {"launches_checked": len(kept), "tiles_checked": checked, "tiles_exact": exact})
 
 
-def _quantize_timed(W, H, K, cs, keep=2):
+def _quantize_timed(Ws, H, K, cs, keep=2):
+    """quantize_linear_group of the weights Ws (one weight: quantize_linear)
+    timed on the wall clock, with the encode sample captured."""
     torch.cuda.synchronize()
     with _LaunchCapture(keep) as cap:
         t0 = time.perf_counter()
-        r = xq.quantize_linear(W, H, K=K, device="cuda", margin=0, channel_scales=cs)
+        rs = xq.quantize_linear_group(Ws, H, K=K, device="cuda", margin=0, channel_scales=cs)
         torch.cuda.synchronize()
         dt = time.perf_counter() - t0
-    return r, dt, cap
+    return rs, dt, cap
 
 
 def _proxy_loss(W, W_hat, H) -> float:
@@ -248,7 +250,7 @@ def _proxy_loss(W, W_hat, H) -> float:
 
 
 def _config_entry(W, H, K, cs, label):
-    r, dt, cap = _quantize_timed(W, H, K, cs)
+    (r,), dt, cap = _quantize_timed([W], H, K, cs)
     tiles = W.numel() // 256
     cb, chk = cpu_baseline_config(cap.kept, tiles)
     e = {"workload": label, "K": K, "seconds": round(dt, 3), "tiles": tiles,
@@ -293,17 +295,40 @@ def run_configs(names):
         H = w["H"].to(dev)
         entry = {"workload": "c4 fused qkv: q 6144x5120 K=5, k/v 1024x5120 K=7, channel "
                              "scales, EXL3 write + reconstruct + fused M=1 GEMV", "members": {}}
+        # members that share K are quantized side by side in one BlockLDLQ
+        # sweep (quantize_linear_group: results identical to separate calls;
+        # k and v have 64 tile columns each, a quarter of the GPU apiece)
+        groups = {}
+        for m in w["members"]:
+            groups.setdefault(m["K"], []).append(m)
+        entry["groups"] = []
         import tempfile
         with tempfile.TemporaryDirectory() as td:
             total, Ws = 0.0, []
-            for m in w["members"]:
-                Wm = m["W"].float().to(dev)
-                e, r = _config_entry(Wm, H, m["K"], True, f"c4 {m['module']} K={m['K']}")
-                entry["members"][m["module"]] = e
-                total += e["seconds"]
-                t0 = time.perf_counter()
-                ex.write_quantized(td, 0, m["module"], r)
-                entry["members"][m["module"]]["write_s"] = round(time.perf_counter() - t0, 3)
+            for K, ms in groups.items():
+                Wg = [m["W"].float().to(dev) for m in ms]
+                rs, dt, cap = _quantize_timed(Wg, H, K, True)
+                tiles = sum(W_.numel() for W_ in Wg) // 256
+                cb, chk = cpu_baseline_config(cap.kept, tiles)
+                label = " + ".join(m["module"] for m in ms)
+                ge = {"members": [m["module"] for m in ms], "K": K, "seconds": round(dt, 3),
+                      "tiles": tiles, "tiles_per_s": round(tiles / dt, 1), "cpu_baseline": cb,
+                      "bit_exact_pct": round(100.0 * chk["tiles_exact"] /
+                                             max(1, chk["tiles_checked"]), 3),
+                      "bit_exact_tiles": chk}
+                entry["groups"].append(ge)
+                total += dt
+                for m, W_, r in zip(ms, Wg, rs):
+                    e = {"K": K, "tiles": W_.numel() // 256,
+                         "proxy_loss": _proxy_loss(W_, r["W_hat"], H)}
+                    t0 = time.perf_counter()
+                    ex.write_quantized(td, 0, m["module"], r)
+                    e["write_s"] = round(time.perf_counter() - t0, 3)
+                    entry["members"][m["module"]] = e
+                log(f"config c4 {label} K={K}: {dt:.3f} s, {tiles / dt:,.0f} tiles/s, proxy "
+                    + ", ".join(f"{entry['members'][m['module']]['proxy_loss']:.3e}" for m in ms)
+                    + f", bit-exact {ge['bit_exact_pct']}% of {chk['tiles_checked']}")
+                del Wg
             inputs = ex.collect_inputs(td)
             for m in w["members"]:
                 base = f"model.language_model.layers.0.{m['module']}"

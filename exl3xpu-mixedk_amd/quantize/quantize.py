@@ -444,8 +444,39 @@ def quantize_linear(W: torch.Tensor, H_x: torch.Tensor | None, code: str = "exl3
     trellis int16 [in/16, out/16, 16K], suh/svh fp16 and diagnostics.
     channel_scales=True applies EXL3 1.4.2's per-channel scaling order.
     """
-    m_out, k_in = W.shape
-    assert k_in % 128 == 0 and m_out % 128 == 0, (W.shape, "need k%128, n%128")
+    return quantize_linear_group(
+        [W], H_x, code=code, K=K, L=L, V=V, percdamp=percdamp, su_seed=su_seed,
+        buf_cols=buf_cols, use_ldlq=use_ldlq, device=device, batch=batch, dtype=dtype,
+        margin=margin, compiled=compiled, progress=progress, backend=backend,
+        channel_scales=channel_scales)[0]
+
+
+def quantize_linear_group(Ws, H_x: torch.Tensor | None, code: str = "exl3_mul1",
+                          K: int = 4, L: int = 16, V: int = 0, percdamp: float = 0.01,
+                          su_seed: int = 20261011, buf_cols: int = 128,
+                          use_ldlq: bool = True, device: str = "cpu",
+                          batch: int = 0, dtype: torch.dtype = torch.float32,
+                          margin: int = 0, compiled: bool = False, progress=None,
+                          backend: str = "hip", channel_scales: bool = False):
+    """quantize_linear for several weights that read the same input (one
+    H_x, e.g. the q/k/v or gate/up projections of a layer) at the same K.
+
+    The block-LDL factor is computed once and the members' inner weights are
+    quantized side by side in one BlockLDLQ sweep: the sweep's feedback only
+    mixes rows within an output column, so the members never interact.  With
+    the column-chain schedule (GPU tensors) every result is bit-identical to
+    a separate quantize_linear call; narrow members (out/16 below the GPU's
+    compute-unit count) then share the GPU instead of leaving most of it
+    idle.  Returns the list of quantize_linear result dicts, in order.
+    """
+    Ws = list(Ws)
+    if not Ws:
+        raise ValueError("quantize_linear_group needs at least one weight")
+    k_in = Ws[0].shape[1]
+    for W in Ws:
+        if W.dim() != 2 or W.shape[1] != k_in:
+            raise ValueError(f"all weights must be [out, {k_in}], got {tuple(W.shape)}")
+        assert k_in % 128 == 0 and W.shape[0] % 128 == 0, (W.shape, "need k%128, n%128")
     if backend not in BACKENDS:
         raise ValueError(f"backend {backend!r} not in {BACKENDS}")
     dev = torch.device(device)
@@ -453,32 +484,41 @@ def quantize_linear(W: torch.Tensor, H_x: torch.Tensor | None, code: str = "exl3
     V = 1 if V == 0 else V
     lut_rms = lut.double().square().mean().sqrt().float()
 
-    suh = sign_vec(k_in, su_seed, dev).half()
-    svh = sign_vec(m_out, su_seed + 1, dev).half()
+    suh0 = sign_vec(k_in, su_seed, dev).half()
     h = hadamard128(dev, torch.float32)
-    W32 = W.float().to(dev).t().contiguous()          # [k, n]
-    if channel_scales:
-        su, sv = suh.float(), svh.float()
-        r_out = W32.square().mean(dim=0).sqrt()
-        rm = r_out.mean()
-        if rm > 1e-30:
-            r_out = r_out / rm
-        zero_out = r_out.abs() < 1e-30
-        r_out = torch.where(zero_out, torch.full_like(r_out, 0.1), r_out)
-        w = had_right(W32 / (sv * r_out).unsqueeze(0), h)
-        r_in = w.square().mean(dim=1).sqrt()
-        r_in = torch.where(r_in.abs() < 1e-30, torch.full_like(r_in, 0.1), r_in)
-        W_i = had_left(w / (su * r_in).unsqueeze(1), h)
-        svh_store = torch.where(zero_out, torch.zeros_like(r_out), r_out)
-    else:
-        W_i = to_inner(W32, suh, svh, h)
-    Wscale = W_i.square().mean().sqrt() / lut_rms
-    Wq = W_i / Wscale
+    members = []
+    for W in Ws:
+        m_out = W.shape[0]
+        suh = suh0
+        svh = sign_vec(m_out, su_seed + 1, dev).half()
+        W32 = W.float().to(dev).t().contiguous()          # [k, n]
+        mb = {"n": m_out}
+        if channel_scales:
+            su, sv = suh.float(), svh.float()
+            r_out = W32.square().mean(dim=0).sqrt()
+            rm = r_out.mean()
+            if rm > 1e-30:
+                r_out = r_out / rm
+            zero_out = r_out.abs() < 1e-30
+            r_out = torch.where(zero_out, torch.full_like(r_out, 0.1), r_out)
+            w = had_right(W32 / (sv * r_out).unsqueeze(0), h)
+            r_in = w.square().mean(dim=1).sqrt()
+            r_in = torch.where(r_in.abs() < 1e-30, torch.full_like(r_in, 0.1), r_in)
+            W_i = had_left(w / (su * r_in).unsqueeze(1), h)
+            svh_store = torch.where(zero_out, torch.zeros_like(r_out), r_out)
+            mb.update(su=su, sv=sv, r_in=r_in, svh_store=svh_store)
+        else:
+            W_i = to_inner(W32, suh, svh, h)
+        Wscale = W_i.square().mean().sqrt() / lut_rms
+        mb.update(Wq=W_i / Wscale, Wscale=Wscale, suh=suh, svh=svh)
+        members.append(mb)
+    Wq = members[0]["Wq"] if len(members) == 1 else \
+        torch.cat([mb["Wq"] for mb in members], dim=1)
 
     Lfac = None
     if use_ldlq and H_x is not None:
         t0 = time.time()
-        G = rotate_hessian(H_x.float().to(dev), suh, h)
+        G = rotate_hessian(H_x.float().to(dev), suh0, h)
         dead = G.diagonal() == 0
         if dead.any():
             G[dead, dead] = 1.0
@@ -500,21 +540,28 @@ def quantize_linear(W: torch.Tensor, H_x: torch.Tensor | None, code: str = "exl3
         "pack/unpack round-trip broke state sequence"
     hatW_g = _hb.decode(trellis, K, code=_hb.code_name(code))
     assert torch.equal(hatW_g, hatWq.to(hatW_g.device)), "decode != encoder output"
-    hatW_d = hatW_g.to(dev)
-    if channel_scales:
-        suh = (su * r_in * Wscale).half()
-        svh = (sv * svh_store).half()
-        W_hat = from_inner(hatW_d, suh, svh, h).t().contiguous()
-    else:
-        W_hat = from_inner(hatW_d * Wscale, suh, svh, h).t().contiguous()
-    return {
-        "W_hat": W_hat.cpu(),
-        "trellis": trellis.cpu(),
-        "suh": suh.cpu(), "svh": svh.cpu(),
-        "Wscale": float(Wscale), "lut_rms": float(lut_rms),
-        "code": code, "K": K, "L": L, "V": V, "use_ldlq": use_ldlq,
-        "channel_scales": channel_scales,
-    }
+    out, off = [], 0
+    for mb in members:
+        n = mb["n"]
+        hatW_d = hatW_g[:, off:off + n].contiguous().to(dev)
+        tr = trellis[:, off // 16:(off + n) // 16].contiguous()
+        off += n
+        Wscale, suh, svh = mb["Wscale"], mb["suh"], mb["svh"]
+        if channel_scales:
+            suh = (mb["su"] * mb["r_in"] * Wscale).half()
+            svh = (mb["sv"] * mb["svh_store"]).half()
+            W_hat = from_inner(hatW_d, suh, svh, h).t().contiguous()
+        else:
+            W_hat = from_inner(hatW_d * Wscale, suh, svh, h).t().contiguous()
+        out.append({
+            "W_hat": W_hat.cpu(),
+            "trellis": tr.cpu(),
+            "suh": suh.cpu(), "svh": svh.cpu(),
+            "Wscale": float(Wscale), "lut_rms": float(lut_rms),
+            "code": code, "K": K, "L": L, "V": V, "use_ldlq": use_ldlq,
+            "channel_scales": channel_scales,
+        })
+    return out
 
 
 def hessian_weighted_err(W: torch.Tensor, W_hat: torch.Tensor, H_x: torch.Tensor) -> float:

@@ -181,3 +181,24 @@ def test_chain_vs_block_schedule(xq, monkeypatch):
     same = (res["chain"][0]["trellis"] == res["block"][0]["trellis"]).all(dim=-1).float().mean()
     print(f"proxy chain {e_c:.6e} block {e_b:.6e}, identical tiles {float(same):.3f}")
     assert abs(e_c - e_b) <= 0.01 * e_b
+
+
+@pytest.mark.parametrize("cs,ldlq", [(False, True), (True, True), (True, False)])
+def test_quantize_linear_group_matches_separate(xq, cs, ldlq):
+    """Members quantized side by side in one sweep give exactly the results
+    of separate quantize_linear calls (their column chains never interact)."""
+    import workloads as wl
+    g = torch.Generator().manual_seed(12)
+    H = wl.ar1_gram(256, 512, 0.5, 12)
+    Ws = [0.02 * torch.randn(128, 256, generator=g), 0.03 * torch.randn(256, 256, generator=g),
+          0.02 * torch.randn(128, 256, generator=g)]
+    print(f"case quantize_linear_group cs={cs} ldlq={ldlq}", flush=True)
+    grp = xq.quantize_linear_group(Ws, H, K=5, device="cuda", channel_scales=cs,
+                                   use_ldlq=ldlq)
+    assert len(grp) == len(Ws)
+    for W, r in zip(Ws, grp):
+        s = xq.quantize_linear(W, H, K=5, device="cuda", channel_scales=cs, use_ldlq=ldlq)
+        assert r["trellis"].shape == (256 // 16, W.shape[0] // 16, 16 * 5)
+        for key in ("W_hat", "trellis", "suh", "svh"):
+            assert torch.equal(r[key], s[key]), key
+        assert r["Wscale"] == s["Wscale"]

@@ -129,6 +129,13 @@ def test_unsupported_variants_raise(xq):
         xq.quantize_seq_tailbite(torch.zeros(128, 2), lut, 4, 16)
     with pytest.raises(ValueError):
         xq.ldlq_viterbi(torch.zeros(16, 16), None, lut, 4, 16, backend="dual")
+    with pytest.raises(ValueError):
+        xq.ldlq_viterbi(torch.zeros(16, 16), None, lut, 4, 16, schedule="rows")
+    # group members must share the input dimension (one Hessian)
+    with pytest.raises(ValueError):
+        xq.quantize_linear_group([torch.zeros(128, 256), torch.zeros(128, 128)], None)
+    with pytest.raises(ValueError):
+        xq.quantize_linear_group([], None)
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU behaviour")
@@ -139,3 +146,5 @@ def test_no_cpu_fallback(xq):
         xq.quantize_seq_tailbite(torch.zeros(256, 2), lut, 4, 16)
     with pytest.raises(RuntimeError):
         xq.quantize_linear(torch.randn(128, 128), None, K=4)
+    with pytest.raises(RuntimeError):
+        xq.ldlq_viterbi(torch.randn(32, 32), None, lut, 4, 16, schedule="chain")
