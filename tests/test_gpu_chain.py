@@ -202,3 +202,17 @@ def test_quantize_linear_group_matches_separate(xq, cs, ldlq):
         for key in ("W_hat", "trellis", "suh", "svh"):
             assert torch.equal(r[key], s[key]), key
         assert r["Wscale"] == s["Wscale"]
+
+
+def test_to_host_staging(xq):
+    """The staged device-to-host copy equals .cpu() for sizes around and
+    across the staging chunks, for several dtypes."""
+    C = xq._STAGE_BYTES
+    for nbytes, dt in ((4 * C, torch.float32), (4 * C + 4, torch.float32),
+                       (9 * C + 2 * 7, torch.int16), (5 * C - 8, torch.float64)):
+        n = nbytes // torch.tensor([], dtype=dt).element_size()
+        t = torch.randn(n, device="cuda").to(dt) if dt.is_floating_point else \
+            torch.randint(-30000, 30000, (n,), device="cuda", dtype=dt)
+        h = xq._to_host(t.view(-1, 1) if n % 2 else t.view(2, -1))
+        assert h.device.type == "cpu" and not h.is_pinned()
+        assert torch.equal(h.view(-1), t.cpu())
