@@ -93,9 +93,9 @@ struct DevCtx {
     size_t seq_cap = 0;
     int32_t* counter = nullptr;  // fused tail-bite: task counter
     uint32_t epoch = 0;          // fused tail-bite: value the current launch publishes
-    float* E = nullptr;          // column chains: (W - What)^T of finished tiles [n][k]
+    float* E = nullptr;          // column chains: W - What of finished tiles (quad layout)
     size_t e_cap = 0;            // floats
-    float* Lt = nullptr;         // column chains: transposed block-LDL factor [k][k]
+    float* Lt = nullptr;         // column chains: block-LDL factor (quad layout)
     size_t lt_cap = 0;           // floats
     uint32_t* cflags = nullptr;  // column chains: tile-ready flags
     size_t cflags_cap = 0;

@@ -464,6 +464,68 @@ __device__ __forceinline__ void tb_chase(const uint8_t* __restrict__ bpq, int ns
     __syncthreads();
 }
 
+// tb_chase for a 1024-thread workgroup with a fixed 64 KiB staging area and
+// the next two chunks' loads in flight in registers while thread 0 chases
+// the current chunk (per chunk: store, barrier, issue the load two chunks
+// ahead, chase), so the chase rather than the load latency sets the pace.
+// Same contract as tb_chase.
+constexpr int kTbStage = 65536;
+
+// Loads chunk c (slots lo .. hi, 64 KiB at most) of a tb_chase_pf run into
+// this thread's four registers.
+template <int K>
+__device__ __forceinline__ void tb_chunk_load(const uint8_t* __restrict__ bpq, int nsteps,
+                                              int stop, int nc, int c, int tid, uint4& r0,
+                                              uint4& r1, uint4& r2, uint4& r3) {
+    using G = Geom<K>;
+    constexpr int CH = kTbStage / G::BPSTEP;
+    if (c >= nc) return;
+    const int hi = nsteps - 2 - c * CH, lo = (hi - CH + 1 > stop) ? hi - CH + 1 : stop;
+    const int n16 = (hi - lo + 1) * (G::BPSTEP / 16);
+    const uint4* src = (const uint4*)(bpq + (size_t)lo * G::BPSTEP);
+    if (tid < n16) r0 = src[tid];
+    if (tid + kFwdThreads < n16) r1 = src[tid + kFwdThreads];
+    if (tid + 2 * kFwdThreads < n16) r2 = src[tid + 2 * kFwdThreads];
+    if (tid + 3 * kFwdThreads < n16) r3 = src[tid + 3 * kFwdThreads];
+}
+
+template <int K>
+__device__ __forceinline__ void tb_chase_pf(const uint8_t* __restrict__ bpq, int nsteps,
+                                            int stop, uint4* stage, int32_t* st,
+                                            int32_t& cur) {
+    using G = Geom<K>;
+    constexpr int CH = kTbStage / G::BPSTEP;           // slots per chunk
+    static_assert(kTbStage / 16 == 4 * kFwdThreads, "four uint4 per thread per chunk");
+    const int tid = threadIdx.x;
+    const int nc = (nsteps - 1 - stop + CH - 1) / CH;  // slots stop .. nsteps-2
+    uint4 a0, a1, a2, a3, b0, b1, b2, b3;
+    tb_chunk_load<K>(bpq, nsteps, stop, nc, 0, tid, a0, a1, a2, a3);
+    tb_chunk_load<K>(bpq, nsteps, stop, nc, 1, tid, b0, b1, b2, b3);
+    for (int c = 0; c < nc; ++c) {
+        const int hi = nsteps - 2 - c * CH, lo = (hi - CH + 1 > stop) ? hi - CH + 1 : stop;
+        const int n16 = (hi - lo + 1) * (G::BPSTEP / 16);
+        __syncthreads();                                // previous chase done with stage
+        if (tid < n16) stage[tid] = a0;
+        if (tid + kFwdThreads < n16) stage[tid + kFwdThreads] = a1;
+        if (tid + 2 * kFwdThreads < n16) stage[tid + 2 * kFwdThreads] = a2;
+        if (tid + 3 * kFwdThreads < n16) stage[tid + 3 * kFwdThreads] = a3;
+        __syncthreads();
+        a0 = b0; a1 = b1; a2 = b2; a3 = b3;
+        tb_chunk_load<K>(bpq, nsteps, stop, nc, c + 2, tid, b0, b1, b2, b3);
+        if (tid == 0) {
+            int s = cur;
+            for (int sl = hi; sl >= lo; --sl) {
+                const int j = (s >> K) & (G::SP - 1);
+                const uint8_t* row = (const uint8_t*)stage + (size_t)(sl - lo) * G::BPSTEP;
+                s = j + bp_lookup<K>(row, j) * G::SP;
+                if (st) st[sl] = s;
+            }
+            cur = s;
+        }
+    }
+    __syncthreads();
+}
+
 // Word wd of one sequence's packed EXL3 trellis, from its states st[0..255]:
 // symbol t = s_t mod 2^K at stream bits [tK, (t+1)K), MSB first; 32-bit
 // words MSB first (quantize.py:360-378).
@@ -711,57 +773,68 @@ __global__ __launch_bounds__(64) void pack_kernel(const int32_t* __restrict__ st
 // so tile (i, j) depends only on tile (i+1, j): the columns are independent
 // chains.  Each of the persistent workgroups takes tile tasks from an atomic
 // counter in sweep order (block tk-1 first), waits (acquire, bounded) for
-// the tile above in its column, computes the targets (the L and E columns
-// read as contiguous rows of their transposes Lt = L^T and Et = E^T, staged
-// through LDS), runs both tail-biting passes with in-workgroup tracebacks,
+// the tile above in its column, computes the targets (the L and E column
+// blocks read in the matrix-core operand layout described below), runs
+// both tail-biting passes with in-workgroup tracebacks,
 // writes the states, the packed trellis, What and E for the tile, and
 // publishes the tile with a release store of the launch's epoch.  A task
 // only waits for a task taken before it, whose workgroup is running, so the
 // waits always end; columns advance independently, so the GPU is not left
 // half idle at the end of every block the way block-synchronous launches of
-// tn tiles are.  The feedback sums run in a fixed order of this kernel
-// (4 partial sums per element, one per quarter of each 128-row chunk, m
-// ascending, added pairwise at the end), not the reference's
-// lazily buffered GEMMs; the encode of each tile is bit-exact for the
-// targets it was given (xdump exposes them).
-constexpr int kChainRows = 128;    // L/E rows staged per feedback chunk
-constexpr int kChainDepth = 4;     // feedback chunks in flight per thread
-constexpr int kChainPad = kChainRows + 4;   // LDS row of a staged chunk
+// tn tiles are.  The feedback is a 16x16 product over m on the matrix
+// cores (v_mfma_f32_16x16x4_f32): wave w accumulates the 16-value groups of
+// m congruent to w mod 16, in ascending order, and the 16 wave partials are
+// added in a fixed tree -- a fixed order of this kernel, not the
+// reference's lazily buffered GEMMs; the encode of each tile is bit-exact
+// for the targets it was given (xdump exposes them).
+constexpr int kChainDepth = 4;     // feedback m-groups in flight per wave
 
-// dst = src^T for a square [k][k] fp32 matrix, only the 64x64 tiles that
-// hold some element with row > column of src (the part the feedback reads).
-__global__ __launch_bounds__(256) void transpose_lower_kernel(const float* __restrict__ src,
-                                                              int k, float* __restrict__ dst) {
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// Operand layout of the feedback ("quad layout"): a [k][n] matrix M is
+// stored per 16-column block b as a [k/4][16][4] array,
+//     Mq[b*16k + (m/4)*64 + 4c + m%4] = M[m][16b + c],
+// so the 4 consecutive m of one column are one float4 and the 16 columns x
+// 16 m of a feedback group are 1 KiB contiguous.  This kernel writes the
+// block-LDL factor L [k][k] in that layout (only the 64x64 tiles holding
+// some element with row > column, the part the feedback reads).
+__global__ __launch_bounds__(256) void lfac_quads_kernel(const float* __restrict__ L, int k,
+                                                         float* __restrict__ Lq) {
     __shared__ float tile[64][65];
-    const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;   // src column / row block
+    const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;   // column / row block of L
     if (r0 + 64 <= c0) return;                               // strictly above the diagonal
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
     for (int yy = ty; yy < 64; yy += 4) {
         const int r = r0 + yy, c = c0 + tx;
-        if (r < k && c < k) tile[yy][tx] = src[(size_t)r * k + c];
+        if (r < k && c < k) tile[yy][tx] = L[(size_t)r * k + c];
     }
     __syncthreads();
-    for (int yy = ty; yy < 64; yy += 4) {
-        const int r = c0 + yy, c = r0 + tx;                  // dst row = src column
-        if (r < k && c < k) dst[(size_t)r * k + c] = tile[tx][yy];
+    // the tile's 4 column blocks, 64 m each: 1024 contiguous floats per block
+    for (int idx = threadIdx.x; idx < 4 * 1024; idx += 256) {
+        const int ib = idx >> 10, w = idx & 1023;
+        const int mq = w >> 6, c = (w >> 2) & 15, mm = w & 3;
+        const int m = r0 + 4 * mq + mm, col = c0 + 16 * ib + c;
+        if (m < k && col < k)
+            Lq[(size_t)(col >> 4) * 16 * k + (size_t)(m >> 2) * 64 + 4 * c + (m & 3)] =
+                tile[4 * mq + mm][16 * ib + c];
     }
 }
 
 template <int K>
 __global__ __launch_bounds__(kFwdThreads) void ldlq_chain_kernel(
-    const float* __restrict__ W, const float* __restrict__ Lt, int k, int n,
+    const float* __restrict__ W, const float* __restrict__ Lq, int k, int n,
     const uint16_t* __restrict__ lut16, int pivot, int n1, uint8_t* __restrict__ bp,
-    float* __restrict__ xbuf, float* __restrict__ hatW, float* __restrict__ Et,
+    float* __restrict__ xbuf, float* __restrict__ hatW, float* __restrict__ Eq,
     int32_t* __restrict__ states, int16_t* __restrict__ trellis, uint32_t* __restrict__ flags,
     int32_t* __restrict__ counter, uint32_t epoch, int spin_limit, uint32_t* __restrict__ err,
     int xdump, float one) {
     using G = Geom<K>;
     __shared__ FwdSmem<K, 1> sm;
-    // staged feedback chunk: lt[r][m] = L[m0+m][16i+r] = Lt[16i+r][m0+m],
-    // et[c][m] = E[m0+m][16j+c] = Et[16j+c][m0+m] (rows padded)
-    __shared__ __attribute__((aligned(16))) float lt[16][kChainPad];
-    __shared__ __attribute__((aligned(16))) float et[16][kChainPad];
-    __shared__ float part[4][256];
+    __shared__ float part[kFwdThreads / 64][256];     // per-wave feedback partials
+    // traceback staging: the forward's b buffers where they hold 64 KiB
+    constexpr bool kOwnStage = 2 * sizeof(float) * G::SPL < (size_t)kTbStage;
+    __shared__ __attribute__((aligned(16))) uint4 tbstage[kOwnStage ? kTbStage / 16 : 1];
+    uint4* const stage = kOwnStage ? tbstage : (uint4*)&sm.bbuf[0][0][0];
     __shared__ int32_t st[kSteps];
     __shared__ int32_t task, cur, ok;
     const int tid = threadIdx.x;
@@ -792,7 +865,7 @@ __global__ __launch_bounds__(kFwdThreads) void ldlq_chain_kernel(
         // wait for tile (i+1, j) (task t - tn)
         if (tid == 0) {
             int good = 1;
-            if (Lt != nullptr && i + 1 < tk) {
+            if (Lq != nullptr && i + 1 < tk) {
                 const uint32_t* f = flags + (size_t)(i + 1) * tn + j;
                 // relaxed polls (no cache invalidation per poll), one acquire
                 // fence once the flag is seen
@@ -820,58 +893,63 @@ __global__ __launch_bounds__(kFwdThreads) void ldlq_chain_kernel(
         }
         __syncthreads();
         if (!__builtin_amdgcn_readfirstlane(ok)) break;
-        // targets: element e = 16r + c of the tile, 4 partial sums per element
+        // targets: the feedback X_fb[r][c] = sum_m L[m][16i+r] E[m][16j+c]
+        // over m >= 16(i+1) on the matrix cores.  One MFMA 16x16x4 step
+        // takes A[r][q] from lane 16q + r and B[q][c] from lane 16q + c;
+        // lane (q, r) loads the float4 of L[m0+4q .. +3][16i+r] and of
+        // E[m0+4q .. +3][16j+r] (quad layout: one 1 KiB block per operand
+        // per wave) for a 16-value group m0 and feeds its components to 4
+        // steps (step t sums m = m0 + 4q + t over q): one 16-byte load per
+        // operand per lane and 4 MFMAs per group.  The accumulator lane
+        // (q, c) holds rows 4q..4q+3 of column c.
         {
-            const int e = tid & 255, pp = tid >> 8;
-            const int r = e >> 4, c = e & 15;
-            float acc = 0.0f;
-            if (Lt != nullptr && i + 1 < tk) {
-                // Chunks of kChainRows values m of the 16 rows Lt[16i+r]
-                // (threads 0..511) and Et[16j+c] (threads 512..1023): each
-                // row chunk is 512 contiguous bytes, one float4 per thread
-                // per chunk, kChainDepth chunks in flight.  Thread (e, pp)
-                // sums m = pp*32 .. pp*32+31 of every chunk, ascending.
-                const bool isl = tid < 512;
-                const int rr = (tid & 511) >> 5, q = tid & 31;
-                const float* src = isl ? Lt + (size_t)(16 * i + rr) * k + 4 * q
-                                       : Et + (size_t)(16 * j + rr) * k + 4 * q;
-                float* const dst = isl ? &lt[rr][4 * q] : &et[rr][4 * q];
-                const int mstart = 16 * (i + 1);
-                float4 pre[kChainDepth];
+            const int wv = tid >> 6, ln = tid & 63, rr = ln & 15, qq = ln >> 4;
+            v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (Lq != nullptr && i + 1 < tk) {
+                const int mstart = 16 * (i + 1), ngr = (k - mstart) >> 4;
+                const size_t q0 = (size_t)(mstart >> 2) * 64 + 64 * qq + 4 * rr;
+                const float* la = Lq + (size_t)i * 16 * k + q0;
+                const float* eb = Eq + (size_t)j * 16 * k + q0;
+                float4 pa[kChainDepth], pb[kChainDepth];
 #pragma unroll
                 for (int d = 0; d < kChainDepth; ++d) {
-                    const int mb = mstart + d * kChainRows;
-                    pre[d] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                    if (mb + 4 * q < k) pre[d] = *(const float4*)(src + mb);
+                    const int g = wv + 16 * d;
+                    pa[d] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    pb[d] = pa[d];
+                    if (g < ngr) {
+                        pa[d] = *(const float4*)(la + 256 * g);
+                        pb[d] = *(const float4*)(eb + 256 * g);
+                    }
                 }
-                for (int m0 = mstart; m0 < k; m0 += kChainDepth * kChainRows) {
+                for (int g0 = wv; g0 < ngr; g0 += 16 * kChainDepth) {
 #pragma unroll
                     for (int d = 0; d < kChainDepth; ++d) {
-                        const int mb = m0 + d * kChainRows;
-                        if (mb < k) {
-                            __syncthreads();
-                            *(float4*)dst = pre[d];
-                            __syncthreads();
-                            const int mn = mb + kChainDepth * kChainRows;
-                            if (mn + 4 * q < k) pre[d] = *(const float4*)(src + mn);
-                            const int rows = (k - mb) < kChainRows ? (k - mb) : kChainRows;
-                            const int lo = pp * 32, hi = (lo + 32) < rows ? lo + 32 : rows;
-                            for (int mm = lo; mm < hi; mm += 4) {
-                                const float4 a = *(const float4*)&lt[r][mm];
-                                const float4 b = *(const float4*)&et[c][mm];
-                                acc = __builtin_fmaf(a.x, b.x, acc);
-                                acc = __builtin_fmaf(a.y, b.y, acc);
-                                acc = __builtin_fmaf(a.z, b.z, acc);
-                                acc = __builtin_fmaf(a.w, b.w, acc);
+                        const int g = g0 + 16 * d;
+                        if (g < ngr) {
+                            const float4 a = pa[d], b = pb[d];
+                            const int gn = g + 16 * kChainDepth;
+                            if (gn < ngr) {
+                                pa[d] = *(const float4*)(la + 256 * gn);
+                                pb[d] = *(const float4*)(eb + 256 * gn);
                             }
+                            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, acc, 0, 0, 0);
+                            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, acc, 0, 0, 0);
+                            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, acc, 0, 0, 0);
+                            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, acc, 0, 0, 0);
                         }
                     }
                 }
             }
-            part[pp][e] = acc;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) part[wv][(4 * qq + v) * 16 + rr] = acc[v];
             __syncthreads();
             if (tid < 256) {
-                const float fb = (part[0][tid] + part[1][tid]) + (part[2][tid] + part[3][tid]);
+                float p8[8];
+#pragma unroll
+                for (int w = 0; w < 8; ++w) p8[w] = part[w][tid] + part[w + 8][tid];
+#pragma unroll
+                for (int w = 0; w < 4; ++w) p8[w] += p8[w + 4];
+                const float fb = (p8[0] + p8[2]) + (p8[1] + p8[3]);
                 // sequence order: x_t = tile[perm[t]] (quantize.py:684-686)
                 const int pe = tid;                      // tile element handled here
                 const float x = W[(size_t)(16 * i + (pe >> 4)) * n + 16 * j + (pe & 15)] + fb;
@@ -900,8 +978,7 @@ __global__ __launch_bounds__(kFwdThreads) void ldlq_chain_kernel(
             __syncthreads();
             if (pass && tid == 0) st[kSteps - 1] = cur & 0xFFFF;
             __syncthreads();
-            tb_chase<K>(bpw, nst, lo, (uint4*)&sm.bbuf[0][0][0], (int)sizeof(sm.bbuf),
-                        pass ? st : nullptr, cur);
+            tb_chase_pf<K>(bpw, nst, lo, stage, pass ? st : nullptr, cur);
         }
         // outputs of the tile
         const size_t tile = (size_t)i * tn + j;
@@ -911,7 +988,8 @@ __global__ __launch_bounds__(kFwdThreads) void ldlq_chain_kernel(
             const size_t g = (size_t)(16 * i + (pe >> 4)) * n + 16 * j + (pe & 15);
             const float w = (float)__builtin_bit_cast(_Float16, lut16[s]);
             hatW[g] = w;
-            Et[(size_t)(16 * j + (pe & 15)) * k + 16 * i + (pe >> 4)] = W[g] - w;
+            const int m = 16 * i + (pe >> 4);                 // E in the quad layout
+            Eq[(size_t)j * 16 * k + (size_t)(m >> 2) * 64 + 4 * (pe & 15) + (m & 3)] = W[g] - w;
             if (states) states[tile * kSteps + tid] = s;
         } else if (tid < kSteps + 8 * K) {
             const int wd = tid - kSteps;
@@ -1007,20 +1085,20 @@ struct FusedL {
 
 template <int K>
 struct ChainL {
-    static hipError_t run(const float* W, const float* L, float* Lt, int k, int n,
+    static hipError_t run(const float* W, const float* L, float* Lq, int k, int n,
                           const uint16_t* lut16, int pivot, int n1, void* bp, int nwg,
-                          float* xbuf, int xdump, float* hatW, float* Et, int32_t* states,
+                          float* xbuf, int xdump, float* hatW, float* Eq, int32_t* states,
                           int16_t* trellis,
                           uint32_t* flags, int32_t* counter, uint32_t epoch, int spin_limit,
                           uint32_t* err, hipStream_t s) {
         hipLaunchKernelGGL(reset_counter_kernel, dim3(1), dim3(1), 0, s, counter);
         if (L != nullptr) {
             const int nb = (k + 63) / 64;
-            hipLaunchKernelGGL(transpose_lower_kernel, dim3(nb, nb), dim3(256), 0, s, L, k, Lt);
+            hipLaunchKernelGGL(lfac_quads_kernel, dim3(nb, nb), dim3(256), 0, s, L, k, Lq);
         }
         hipLaunchKernelGGL(ldlq_chain_kernel<K>, dim3(nwg), dim3(kFwdThreads), 0, s, W,
-                           L != nullptr ? (const float*)Lt : nullptr, k, n, lut16, pivot, n1,
-                           (uint8_t*)bp, xbuf, hatW, Et, states, trellis, flags, counter, epoch,
+                           L != nullptr ? (const float*)Lq : nullptr, k, n, lut16, pivot, n1,
+                           (uint8_t*)bp, xbuf, hatW, Eq, states, trellis, flags, counter, epoch,
                            spin_limit, err, xdump, 1.0f);
         return hipGetLastError();
     }
@@ -1115,9 +1193,9 @@ hipError_t launch_tailbite_fused(int K, const float* X, int nseq, const uint16_t
                               epoch, spin_limit, err, stream);
 }
 
-hipError_t launch_ldlq_chain(int K, const float* W, const float* L, float* Lt, int k, int n,
+hipError_t launch_ldlq_chain(int K, const float* W, const float* L, float* Lq, int k, int n,
                             const uint16_t* lut16, int pivot, int n1, void* bp, int nwg,
-                            float* xbuf, int xdump, float* hatW, float* Et, int32_t* states,
+                            float* xbuf, int xdump, float* hatW, float* Eq, int32_t* states,
                             int16_t* trellis, uint32_t* flags, int32_t* counter,
                             uint32_t epoch, int spin_limit, uint32_t* err,
                             hipStream_t stream) {
@@ -1125,9 +1203,9 @@ hipError_t launch_ldlq_chain(int K, const float* W, const float* L, float* Lt, i
     if (k % 16 || n % 16 || pivot < 0 || pivot >= kSteps || n1 <= pivot || n1 > kSteps ||
         nwg < 1 || spin_limit < 1)
         return hipErrorInvalidValue;
-    if (L != nullptr && Lt == nullptr) return hipErrorInvalidValue;
-    return dispatch_k<ChainL>(K, W, L, Lt, k, n, lut16, pivot, n1, bp, nwg, xbuf, xdump, hatW,
-                              Et, states, trellis, flags, counter, epoch, spin_limit, err,
+    if (L != nullptr && Lq == nullptr) return hipErrorInvalidValue;
+    return dispatch_k<ChainL>(K, W, L, Lq, k, n, lut16, pivot, n1, bp, nwg, xbuf, xdump, hatW,
+                              Eq, states, trellis, flags, counter, epoch, spin_limit, err,
                               stream);
 }
 

@@ -52,9 +52,10 @@ def _seq_order(T: torch.Tensor, perm: torch.Tensor) -> torch.Tensor:
 
 def _check_targets(W, L, hatW, xt, perm):
     """xt against the fp64 formula on the kernel's What.  The kernel sums each
-    target as 4 fp32 partial sums (one per quarter of every 128-row chunk, so
-    at most k/4 + 32 products each), adds the partials pairwise and then W:
-    its error is below (k/4 + 36) u times |W| + sum |L| |E| (u = 2^-24)."""
+    target as 16 fp32 wave partials of at most k/16 products each (matrix-core
+    steps of 4 products), adds them in a 4-level tree and then W: even with a
+    rounding after every product its error is below (k/16 + 5) u times
+    |W| + sum |L| |E| (u = 2^-24); the check allows (k/4 + 36) u."""
     k, n = W.shape
     W64 = W.double()
     E = (W - hatW).double()              # the kernel's fp32 E, exactly
