@@ -189,13 +189,17 @@ class _LaunchCapture:
         xq.ldlq_viterbi.keep_targets = False
         xt = xq.ldlq_viterbi.last_targets
         if xt is not None and not self.kept:
-            tr = xq.ldlq_viterbi.last_trellis
-            tk, tn, K = tr.shape[0], tr.shape[1], tr.shape[2] // 16
-            st = hb.unpack(tr.reshape(-1, 16 * K), K).view(tk, tn, 256)
+            groups = xq.ldlq_viterbi.last_groups or \
+                [(0, xt.shape[1] * 16, xq.ldlq_viterbi.last_trellis.shape[2] // 16,
+                  xq.ldlq_viterbi.last_trellis)]
+            tk = xt.shape[0]
             rows = sorted({tk - 1 - (r * (tk - 1)) // max(1, self.keep - 1)
                            for r in range(self.keep)}, reverse=True)
-            for i in rows:
-                self.kept.append((xt[i].clone(), st[i].clone(), K, 128, 0))
+            for c0, nc, K, tr in groups:
+                st = hb.unpack(tr.reshape(-1, 16 * K), K).view(tk, nc // 16, 256)
+                for i in rows:
+                    self.kept.append((xt[i, c0 // 16:(c0 + nc) // 16].clone(), st[i].clone(),
+                                      K, 128, 0))
             self.launches = 1
             xq.ldlq_viterbi.last_targets = None
 
@@ -295,23 +299,21 @@ def run_configs(names):
         H = w["H"].to(dev)
         entry = {"workload": "c4 fused qkv: q 6144x5120 K=5, k/v 1024x5120 K=7, channel "
                              "scales, EXL3 write + reconstruct + fused M=1 GEMV", "members": {}}
-        # members that share K are quantized side by side in one BlockLDLQ
-        # sweep (quantize_linear_group: results identical to separate calls;
-        # k and v have 64 tile columns each, a quarter of the GPU apiece)
-        groups = {}
-        for m in w["members"]:
-            groups.setdefault(m["K"], []).append(m)
+        # the members share H and are quantized side by side in one sweep
+        # (quantize_linear_group with their K each: results identical to
+        # separate calls; the K=5 and K=7 columns run as concurrent launches)
+        groups = {tuple(m["K"] for m in w["members"]): w["members"]}
         entry["groups"] = []
         import tempfile
         with tempfile.TemporaryDirectory() as td:
             total, Ws = 0.0, []
             for K, ms in groups.items():
                 Wg = [m["W"].float().to(dev) for m in ms]
-                rs, dt, cap = _quantize_timed(Wg, H, K, True)
+                rs, dt, cap = _quantize_timed(Wg, H, list(K), True)
                 tiles = sum(W_.numel() for W_ in Wg) // 256
                 cb, chk = cpu_baseline_config(cap.kept, tiles)
                 label = " + ".join(m["module"] for m in ms)
-                ge = {"members": [m["module"] for m in ms], "K": K, "seconds": round(dt, 3),
+                ge = {"members": [m["module"] for m in ms], "K": list(K), "seconds": round(dt, 3),
                       "tiles": tiles, "tiles_per_s": round(tiles / dt, 1), "cpu_baseline": cb,
                       "bit_exact_pct": round(100.0 * chk["tiles_exact"] /
                                              max(1, chk["tiles_checked"]), 3),
@@ -319,13 +321,13 @@ def run_configs(names):
                 entry["groups"].append(ge)
                 total += dt
                 for m, W_, r in zip(ms, Wg, rs):
-                    e = {"K": K, "tiles": W_.numel() // 256,
+                    e = {"K": m["K"], "tiles": W_.numel() // 256,
                          "proxy_loss": _proxy_loss(W_, r["W_hat"], H)}
                     t0 = time.perf_counter()
                     ex.write_quantized(td, 0, m["module"], r)
                     e["write_s"] = round(time.perf_counter() - t0, 3)
                     entry["members"][m["module"]] = e
-                log(f"config c4 {label} K={K}: {dt:.3f} s, {tiles / dt:,.0f} tiles/s, proxy "
+                log(f"config c4 {label} K={list(K)}: {dt:.3f} s, {tiles / dt:,.0f} tiles/s, proxy "
                     + ", ".join(f"{entry['members'][m['module']]['proxy_loss']:.3e}" for m in ms)
                     + f", bit-exact {ge['bit_exact_pct']}% of {chk['tiles_checked']}")
                 del Wg

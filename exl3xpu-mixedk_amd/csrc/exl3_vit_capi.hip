@@ -80,6 +80,9 @@ int parse_code(const char* code, Code* out) {
 }
 
 // ------------------------------------------------------------ device state
+// Column groups of different K in one chain call (each its own launch).
+constexpr int kMaxChainGroups = 8;
+
 struct DevCtx {
     bool ready = false;
     int ncu = 0;
@@ -101,6 +104,9 @@ struct DevCtx {
     size_t cflags_cap = 0;
     float* xbuf = nullptr;       // column chains: each workgroup's target row
     size_t xbuf_cap = 0;         // floats
+    int32_t* ccount = nullptr;   // column chains: one task counter per concurrent launch
+    hipStream_t side[kMaxChainGroups - 1] = {};   // launches of groups 1.. of a call
+    hipEvent_t fork = nullptr, join[kMaxChainGroups - 1] = {};
     float* hx = nullptr;       // staging for the host-pointer entries
     int32_t* hs = nullptr;
     size_t host_cap = 0;
@@ -428,19 +434,84 @@ int run_tailbite(DevCtx& cx, const float* dX, int nseq, int K, Code code, int ma
     return scratch_end(cx, s, sync);
 }
 
-// The BlockLDLQ sweep as column chains in one persistent launch (see
-// ldlq_chain_kernel): library-owned E, tile flags, per-workgroup
+// Relative cost of one tile of the chain kernel per K (measured kernel
+// times of the 5120x5120 sweep), for splitting the CUs between groups.
+double chain_tile_cost(int K) {
+    static const double c[8] = {1.0, 1.0, 1.09, 1.0, 1.0, 1.07, 1.04, 1.08};
+    return (K >= 2 && K <= 7) ? c[K] : 1.0;
+}
+
+// Workgroups per group: proportional to the group's work, at most one per
+// column chain, at least one, summing to at most ncu.
+void split_cus(int ncu, int ng, const int* tng, const int* Kg, int tk, int* nwg) {
+    if (ng == 1) {
+        nwg[0] = ncu;
+        return;
+    }
+    double w[kMaxChainGroups], tot = 0.0;
+    bool capped[kMaxChainGroups] = {};
+    for (int g = 0; g < ng; ++g) tot += (w[g] = (double)tng[g] * tk * chain_tile_cost(Kg[g]));
+    int left = ncu;
+    // water-filling: groups with fewer chains than their share keep one
+    // workgroup per chain and give the rest to the others
+    for (bool again = true; again;) {
+        again = false;
+        double wt = 0.0;
+        for (int g = 0; g < ng; ++g)
+            if (!capped[g]) wt += w[g];
+        for (int g = 0; g < ng; ++g) {
+            if (capped[g]) continue;
+            if (wt > 0 && (double)left * w[g] / wt > tng[g]) {
+                capped[g] = true;
+                nwg[g] = tng[g];
+                left -= tng[g];
+                again = true;
+            }
+        }
+        if (!again) {
+            int used = 0, big = -1;
+            for (int g = 0; g < ng; ++g) {
+                if (capped[g]) continue;
+                nwg[g] = (int)((double)left * w[g] / (wt > 0 ? wt : 1.0));
+                if (nwg[g] < 1) nwg[g] = 1;
+                used += nwg[g];
+                if (big < 0 || w[g] > w[big]) big = g;
+            }
+            if (big >= 0) nwg[big] += left - used;       // rounding remainder
+            for (int g = 0; g < ng; ++g)
+                if (nwg[g] < 1) nwg[g] = 1;
+        }
+    }
+    (void)tot;
+}
+
+struct ChainGroup { int jc0, tnl, K; int16_t* trellis; };
+
+// The BlockLDLQ sweep as column chains (see ldlq_chain_kernel): the factor
+// repacked once, then one persistent launch per column group, the first on
+// the caller's stream and the others concurrently on library streams, with
+// the CUs split by work.  Library-owned E, tile flags, per-workgroup
 // backpointer slots and target rows.
-int run_ldlq_chain(DevCtx& cx, const float* W, const float* L, int k, int n, int K, Code code,
-                   int margin, int pivot, float* hatW, int32_t* states, int16_t* trellis,
-                   float* targets, hipStream_t s) {
-    const size_t ntile = (size_t)(k / 16) * (size_t)(n / 16);
-    const int nwg = cx.ncu > 0 ? cx.ncu : 1;     // one 1024-thread workgroup per CU
-    int rc = reserve_scratch(cx, K, nwg);
-    if (rc) return rc;
-    const size_t need_e = (size_t)k * n, need_x = targets ? 0 : (size_t)nwg * xtq::kSteps;
+int run_ldlq_chain(DevCtx& cx, const float* W, const float* L, int k, int n,
+                   const ChainGroup* grp, int ng, Code code, int margin, int pivot,
+                   float* hatW, int32_t* states, float* targets, hipStream_t s) {
+    const int tk = k / 16;
+    const size_t ntile = (size_t)tk * (size_t)(n / 16);
+    int tng[kMaxChainGroups], Kg[kMaxChainGroups], nwg[kMaxChainGroups];
+    for (int g = 0; g < ng; ++g) { tng[g] = grp[g].tnl; Kg[g] = grp[g].K; }
+    split_cus(cx.ncu > 0 ? cx.ncu : 1, ng, tng, Kg, tk, nwg);
+    size_t bp_bytes = 0, xrows = 0;
+    size_t bp_off[kMaxChainGroups], x_off[kMaxChainGroups];
+    for (int g = 0; g < ng; ++g) {
+        bp_off[g] = bp_bytes;
+        x_off[g] = xrows;
+        bp_bytes += (size_t)nwg[g] * xtq::bp_tile_bytes(Kg[g]);
+        xrows += (size_t)nwg[g];
+    }
+    const size_t need_e = (size_t)k * n, need_x = targets ? 0 : xrows * xtq::kSteps;
     const size_t need_lt = L ? (size_t)k * k : 0;
     size_t add = 0;
+    if (bp_bytes > cx.bp_cap) add += bp_bytes - cx.bp_cap;
     if (need_e > cx.e_cap) add += (need_e - cx.e_cap) * sizeof(float);
     if (need_lt > cx.lt_cap) add += (need_lt - cx.lt_cap) * sizeof(float);
     if (ntile > cx.cflags_cap) add += (ntile - cx.cflags_cap) * sizeof(uint32_t);
@@ -450,6 +521,11 @@ int run_ldlq_chain(DevCtx& cx, const float* W, const float* L, int k, int n, int
         return 5;
     }
     if (add && hipEventSynchronize(cx.last) != hipSuccess) return 4;
+    {
+        size_t cap = cx.bp_cap;
+        if (grow((uint8_t**)&cx.bp, &cap, bp_bytes, 1, &cx.owned)) return 2;
+        cx.bp_cap = cap;
+    }
     if (grow(&cx.E, &cx.e_cap, need_e, sizeof(float), &cx.owned)) return 2;
     if (grow(&cx.Lt, &cx.lt_cap, need_lt, sizeof(float), &cx.owned)) return 2;
     if (ntile > cx.cflags_cap) {
@@ -457,18 +533,49 @@ int run_ldlq_chain(DevCtx& cx, const float* W, const float* L, int k, int n, int
         if (hipMemset(cx.cflags, 0, ntile * sizeof(uint32_t)) != hipSuccess) return 4;
     }
     if (grow(&cx.xbuf, &cx.xbuf_cap, need_x, sizeof(float), &cx.owned)) return 2;
-    rc = scratch_begin(cx, s);
+    if (!cx.ccount) {
+        if (hipMalloc((void**)&cx.ccount, kMaxChainGroups * sizeof(int32_t)) != hipSuccess)
+            return 2;
+        cx.owned += kMaxChainGroups * sizeof(int32_t);
+    }
+    for (int g = 1; g < ng; ++g) {
+        if (!cx.side[g - 1] &&
+            (hipStreamCreateWithFlags(&cx.side[g - 1], hipStreamNonBlocking) != hipSuccess ||
+             hipEventCreateWithFlags(&cx.join[g - 1], hipEventDisableTiming) != hipSuccess))
+            return 1;
+    }
+    if (ng > 1 && !cx.fork && hipEventCreateWithFlags(&cx.fork, hipEventDisableTiming) != hipSuccess)
+        return 1;
+    int rc = scratch_begin(cx, s);
     if (rc) return rc;
     if (++cx.epoch == 0) cx.epoch = 1;
     const int n1 = (margin > 0 && pivot + margin < xtq::kSteps) ? pivot + margin : xtq::kSteps;
-    const int pf = prof_begin(s, 0, (double)ntile * (n1 + xtq::kSteps));
-    const hipError_t e = xtq::launch_ldlq_chain(
-        K, W, L, cx.Lt, k, n, cx.lut16[code], pivot, n1, cx.bp, nwg, targets ? targets : cx.xbuf,
-        targets ? 1 : 0, hatW, cx.E, states, trellis, cx.cflags, cx.counter, cx.epoch,
-        kSpinLimit, cx.err, s);
+    double steps = 0.0;
+    for (int g = 0; g < ng; ++g) steps += (double)tk * tng[g] * (n1 + xtq::kSteps);
+    const int pf = prof_begin(s, 0, steps);
+    hipError_t e = hipSuccess;
+    if (L) e = xtq::launch_lfac_quads(L, k, cx.Lt, s);
+    if (e == hipSuccess && ng > 1 && hipEventRecord(cx.fork, s) != hipSuccess) e = hipErrorUnknown;
+    for (int g = 0; g < ng && e == hipSuccess; ++g) {
+        hipStream_t sg = g ? cx.side[g - 1] : s;
+        if (g && hipStreamWaitEvent(sg, cx.fork, 0) != hipSuccess) {
+            e = hipErrorUnknown;
+            break;
+        }
+        e = xtq::launch_ldlq_chain(
+            Kg[g], W, L ? cx.Lt : nullptr, k, n, grp[g].jc0, grp[g].tnl, cx.lut16[code], pivot,
+            n1, (uint8_t*)cx.bp + bp_off[g], nwg[g], targets ? targets : cx.xbuf + x_off[g] * xtq::kSteps,
+            targets ? 1 : 0, hatW, cx.E, states, grp[g].trellis, cx.cflags, cx.ccount + g,
+            cx.epoch, kSpinLimit, cx.err, sg);
+        if (e == hipSuccess && g &&
+            (hipEventRecord(cx.join[g - 1], sg) != hipSuccess ||
+             hipStreamWaitEvent(s, cx.join[g - 1], 0) != hipSuccess))
+            e = hipErrorUnknown;
+    }
     prof_end(pf, s);
     if (e != hipSuccess) {
         fprintf(stderr, "xtq_vit ldlq chain: %s\n", hipGetErrorString(e));
+        (void)hipDeviceSynchronize();
         return 4;
     }
     return scratch_end(cx, s, true);
@@ -650,24 +757,43 @@ int xtq_vit_status_dev(void* stream) {
 int xtq_ldlq_chain_dev(const float* d_W, const float* d_L, int k, int n, int K,
                        const char* code, int margin, int pivot, float* d_hatW,
                        int32_t* d_states, int16_t* d_trellis, float* d_targets, void* stream) {
+    int16_t* tr[1] = {d_trellis};
+    return xtq_ldlq_chain_multi_dev(d_W, d_L, k, n, 1, &n, &K, code, margin, pivot, d_hatW,
+                                    d_states, tr, d_targets, stream);
+}
+
+int xtq_ldlq_chain_multi_dev(const float* d_W, const float* d_L, int k, int n, int ngroups,
+                             const int* h_ncols, const int* h_K, const char* code, int margin,
+                             int pivot, float* d_hatW, int32_t* d_states,
+                             int16_t* const* h_trellis, float* d_targets, void* stream) {
     std::lock_guard<std::mutex> lk(g_mu);
-    if (!d_W || !d_hatW || !d_trellis) return 12;
+    if (!d_W || !d_hatW || !h_ncols || !h_K || !h_trellis) return 12;
     Code c;
     int rc = parse_code(code, &c);
     if (rc) return rc;
     read_env();
-    if (K < 2 || K > 7) return 9;
+    if (ngroups < 1 || ngroups > kMaxChainGroups) return 6;
+    ChainGroup grp[kMaxChainGroups];
+    int col = 0;
+    for (int g = 0; g < ngroups; ++g) {
+        if (h_K[g] < 2 || h_K[g] > 7) return 9;
+        if (!h_trellis[g]) return 12;
+        if (h_ncols[g] <= 0 || h_ncols[g] % 16) return 6;
+        grp[g] = ChainGroup{col / 16, h_ncols[g] / 16, h_K[g], h_trellis[g]};
+        col += h_ncols[g];
+    }
     if (pivot < 0 || pivot >= xtq::kSteps || margin < 0) return 10;
     if (d_L && ((uintptr_t)d_L & 15)) return 12;     // rows are read as float4
-    if (k <= 0 || n <= 0 || k % 16 || n % 16 ||
-        (long long)(k / 16) * (n / 16) > g_maxseq || (long long)k * n > (1LL << 31) - 1)
+    if (k <= 0 || n <= 0 || k % 16 || n % 16 || col != n ||
+        (long long)(k / 16) * (n / 16) > g_maxseq || (long long)k * n > (1LL << 31) - 1 ||
+        (long long)k * k > (1LL << 31) - 1)
         return 6;
     int dev = 0;
     if (current_device(&dev)) return 1;
     rc = dev_init(dev);
     if (rc) return rc;
-    return run_ldlq_chain(g_dev[dev], d_W, d_L, k, n, K, c, margin, pivot, d_hatW, d_states,
-                          d_trellis, d_targets, (hipStream_t)stream);
+    return run_ldlq_chain(g_dev[dev], d_W, d_L, k, n, grp, ngroups, c, margin, pivot, d_hatW,
+                          d_states, d_targets, (hipStream_t)stream);
 }
 
 int xtq_vit_viterbi_dev(const float* dX, int nseq, int T, int K, const char* code,

@@ -58,24 +58,30 @@ hipError_t launch_tailbite_fused(int K, const float* X, int nseq, const uint16_t
                                  uint32_t* flags, int32_t* counter, uint32_t epoch,
                                  int spin_limit, uint32_t* err, hipStream_t stream);
 
-// The BlockLDLQ sweep of W [k][n] (inner domain, row-major, k and n
-// multiples of 16) as one persistent launch of nwg workgroups over the tile
-// column chains (see ldlq_chain_kernel).  L [k][k] is the block-LDL factor
-// (row-major; NULL: no feedback, plain tail-biting of every tile); Lq (k*k
-// floats of scratch) first receives its lower part in the feedback's quad
-// layout (see lfac_quads_kernel).  Writes hatW [k][n] (decoded tiles), Eq
-// (k*n floats of scratch: W - hatW in the quad layout, which the kernel
-// reads for the feedback), states [tk*tn][256] (nullable) and trellis
-// [tk*tn][16K] in row-block order.  bp: nwg backpointer slots of
+// Writes the block-LDL factor L [k][k] (row-major, k a multiple of 16) into
+// Lq (k*k floats) in the chain feedback's quad layout (see
+// lfac_quads_kernel; only the part below the diagonal blocks).
+hipError_t launch_lfac_quads(const float* L, int k, float* Lq, hipStream_t stream);
+
+// The BlockLDLQ sweep of the column tiles jc0 .. jc0+tnl-1 of W [k][n]
+// (inner domain, row-major, k and n multiples of 16) as one persistent
+// launch of nwg workgroups over their column chains (see ldlq_chain_kernel).
+// Lq: the factor from launch_lfac_quads (NULL: no feedback, plain
+// tail-biting of every tile).  Writes hatW [k][n] (decoded tiles), Eq (k*n
+// floats of scratch: W - hatW in the quad layout, which the kernel reads
+// for the feedback), states [tk*tn][256] (nullable) and trellis
+// [tk][tnl][16K] of the launch's tiles.  bp: nwg backpointer slots of
 // bp_tile_bytes(K); xbuf: the targets, [nwg][256] scratch, or with xdump
 // [tk*tn][256] holding every tile's targets afterwards.  flags [tk*tn] hold
-// values != epoch on entry; counter is one device word.  err |= 1 on a NaN
-// target, |= 2 when a wait expires after spin_limit polls.
-hipError_t launch_ldlq_chain(int K, const float* W, const float* L, float* Lq, int k, int n,
-                             const uint16_t* lut16, int pivot, int n1, void* bp, int nwg,
-                             float* xbuf, int xdump, float* hatW, float* Eq, int32_t* states,
-                             int16_t* trellis, uint32_t* flags, int32_t* counter,
-                             uint32_t epoch, int spin_limit, uint32_t* err,
+// values != epoch on entry; counter is one device word per launch.  Launches
+// over disjoint column ranges may run concurrently (they share Lq, Eq,
+// hatW, states and flags).  err |= 1 on a NaN target, |= 2 when a wait
+// expires after spin_limit polls, |= 4 on a runaway task loop.
+hipError_t launch_ldlq_chain(int K, const float* W, const float* Lq, int k, int n, int jc0,
+                             int tnl, const uint16_t* lut16, int pivot, int n1, void* bp,
+                             int nwg, float* xbuf, int xdump, float* hatW, float* Eq,
+                             int32_t* states, int16_t* trellis, uint32_t* flags,
+                             int32_t* counter, uint32_t epoch, int spin_limit, uint32_t* err,
                              hipStream_t stream);
 
 // Traceback of one run from send (the state at step nsteps-1) down to step

@@ -822,7 +822,7 @@ __global__ __launch_bounds__(256) void lfac_quads_kernel(const float* __restrict
 
 template <int K>
 __global__ __launch_bounds__(kFwdThreads) void ldlq_chain_kernel(
-    const float* __restrict__ W, const float* __restrict__ Lq, int k, int n,
+    const float* __restrict__ W, const float* __restrict__ Lq, int k, int n, int jc0, int tnl,
     const uint16_t* __restrict__ lut16, int pivot, int n1, uint8_t* __restrict__ bp,
     float* __restrict__ xbuf, float* __restrict__ hatW, float* __restrict__ Eq,
     int32_t* __restrict__ states, int16_t* __restrict__ trellis, uint32_t* __restrict__ flags,
@@ -838,7 +838,9 @@ __global__ __launch_bounds__(kFwdThreads) void ldlq_chain_kernel(
     __shared__ int32_t st[kSteps];
     __shared__ int32_t task, cur, ok;
     const int tid = threadIdx.x;
-    const int tk = k / 16, tn = n / 16, ntask = tk * tn;
+    // this launch sweeps the column tiles jc0 .. jc0+tnl-1 of the [k][n]
+    // matrices (its trellis holds just those: [tk][tnl][16K])
+    const int tk = k / 16, tn = n / 16, ntask = tk * tnl;
     // this workgroup's backpointer slot and target row (or the dump row)
     uint8_t* const bpw = bp + (size_t)blockIdx.x * ((size_t)kSlots * G::BPSTEP);
     // Thread 0 publishes a finished tile and fetches the next task in ONE
@@ -859,7 +861,7 @@ __global__ __launch_bounds__(kFwdThreads) void ldlq_chain_kernel(
             if (tid == 0) atomicOr(err, 4u);
             break;
         }
-        const int i = tk - 1 - t / tn, j = t - (t / tn) * tn;
+        const int i = tk - 1 - t / tnl, jl = t - (t / tnl) * tnl, j = jc0 + jl;
         // targets row: the workgroup's own, or the tile's (row-block order)
         float* const xs = xbuf + (xdump ? (size_t)i * tn + j : (size_t)blockIdx.x) * kSteps;
         // wait for tile (i+1, j) (task t - tn)
@@ -993,7 +995,7 @@ __global__ __launch_bounds__(kFwdThreads) void ldlq_chain_kernel(
             if (states) states[tile * kSteps + tid] = s;
         } else if (tid < kSteps + 8 * K) {
             const int wd = tid - kSteps;
-            store_word(trellis + tile * 16 * K + 2 * wd, pack_word<K>(st, wd));
+            store_word(trellis + ((size_t)i * tnl + jl) * 16 * K + 2 * wd, pack_word<K>(st, wd));
         }
         // every wave's stores complete (explicitly: the barrier's
         // workgroup-scope release does not wait for them) before thread 0's
@@ -1085,21 +1087,15 @@ struct FusedL {
 
 template <int K>
 struct ChainL {
-    static hipError_t run(const float* W, const float* L, float* Lq, int k, int n,
+    static hipError_t run(const float* W, const float* Lq, int k, int n, int jc0, int tnl,
                           const uint16_t* lut16, int pivot, int n1, void* bp, int nwg,
                           float* xbuf, int xdump, float* hatW, float* Eq, int32_t* states,
-                          int16_t* trellis,
-                          uint32_t* flags, int32_t* counter, uint32_t epoch, int spin_limit,
-                          uint32_t* err, hipStream_t s) {
+                          int16_t* trellis, uint32_t* flags, int32_t* counter, uint32_t epoch,
+                          int spin_limit, uint32_t* err, hipStream_t s) {
         hipLaunchKernelGGL(reset_counter_kernel, dim3(1), dim3(1), 0, s, counter);
-        if (L != nullptr) {
-            const int nb = (k + 63) / 64;
-            hipLaunchKernelGGL(lfac_quads_kernel, dim3(nb, nb), dim3(256), 0, s, L, k, Lq);
-        }
-        hipLaunchKernelGGL(ldlq_chain_kernel<K>, dim3(nwg), dim3(kFwdThreads), 0, s, W,
-                           L != nullptr ? (const float*)Lq : nullptr, k, n, lut16, pivot, n1,
-                           (uint8_t*)bp, xbuf, hatW, Eq, states, trellis, flags, counter, epoch,
-                           spin_limit, err, xdump, 1.0f);
+        hipLaunchKernelGGL(ldlq_chain_kernel<K>, dim3(nwg), dim3(kFwdThreads), 0, s, W, Lq, k,
+                           n, jc0, tnl, lut16, pivot, n1, (uint8_t*)bp, xbuf, hatW, Eq, states,
+                           trellis, flags, counter, epoch, spin_limit, err, xdump, 1.0f);
         return hipGetLastError();
     }
 };
@@ -1193,19 +1189,26 @@ hipError_t launch_tailbite_fused(int K, const float* X, int nseq, const uint16_t
                               epoch, spin_limit, err, stream);
 }
 
-hipError_t launch_ldlq_chain(int K, const float* W, const float* L, float* Lq, int k, int n,
-                            const uint16_t* lut16, int pivot, int n1, void* bp, int nwg,
-                            float* xbuf, int xdump, float* hatW, float* Eq, int32_t* states,
-                            int16_t* trellis, uint32_t* flags, int32_t* counter,
-                            uint32_t epoch, int spin_limit, uint32_t* err,
+hipError_t launch_lfac_quads(const float* L, int k, float* Lq, hipStream_t stream) {
+    if (k <= 0) return hipSuccess;
+    if (k % 16 || L == nullptr || Lq == nullptr) return hipErrorInvalidValue;
+    const int nb = (k + 63) / 64;
+    hipLaunchKernelGGL(lfac_quads_kernel, dim3(nb, nb), dim3(256), 0, stream, L, k, Lq);
+    return hipGetLastError();
+}
+
+hipError_t launch_ldlq_chain(int K, const float* W, const float* Lq, int k, int n, int jc0,
+                            int tnl, const uint16_t* lut16, int pivot, int n1, void* bp,
+                            int nwg, float* xbuf, int xdump, float* hatW, float* Eq,
+                            int32_t* states, int16_t* trellis, uint32_t* flags,
+                            int32_t* counter, uint32_t epoch, int spin_limit, uint32_t* err,
                             hipStream_t stream) {
-    if (k <= 0 || n <= 0) return hipSuccess;
-    if (k % 16 || n % 16 || pivot < 0 || pivot >= kSteps || n1 <= pivot || n1 > kSteps ||
-        nwg < 1 || spin_limit < 1)
+    if (k <= 0 || n <= 0 || tnl <= 0) return hipSuccess;
+    if (k % 16 || n % 16 || jc0 < 0 || jc0 + tnl > n / 16 || pivot < 0 || pivot >= kSteps ||
+        n1 <= pivot || n1 > kSteps || nwg < 1 || spin_limit < 1)
         return hipErrorInvalidValue;
-    if (L != nullptr && Lq == nullptr) return hipErrorInvalidValue;
-    return dispatch_k<ChainL>(K, W, L, Lq, k, n, lut16, pivot, n1, bp, nwg, xbuf, xdump, hatW,
-                              Eq, states, trellis, flags, counter, epoch, spin_limit, err,
+    return dispatch_k<ChainL>(K, W, Lq, k, n, jc0, tnl, lut16, pivot, n1, bp, nwg, xbuf, xdump,
+                              hatW, Eq, states, trellis, flags, counter, epoch, spin_limit, err,
                               stream);
 }
 

@@ -53,6 +53,8 @@ def lib():
         L.xtq_vit_tailbite_dev_async.argtypes = [vp, i32, i32, cp, i32, i32, vp, vp, vp]
         L.xtq_vit_status_dev.argtypes = [vp]
         L.xtq_ldlq_chain_dev.argtypes = [vp, vp, i32, i32, i32, cp, i32, i32, vp, vp, vp, vp, vp]
+        L.xtq_ldlq_chain_multi_dev.argtypes = [vp, vp, i32, i32, i32, vp, vp, cp, i32, i32,
+                                               vp, vp, vp, vp, vp]
         L.xtq_vit_viterbi_dev.argtypes = [vp, i32, i32, i32, cp, vp, i32, vp, vp]
         L.xtq_trellis_decode_dev.argtypes = [vp, i32, i32, i32, cp, vp, vp, vp]
         L.xtq_trellis_pack_dev.argtypes = [vp, i32, i32, vp, vp]
@@ -72,7 +74,7 @@ def lib():
         L.xtq_vit_strerror.restype = cp
         for fn in ("xtq_vit_init", "xtq_vit_run", "xtq_vit_run_k", "xtq_vit_tailbite_dev",
                    "xtq_vit_tailbite_dev_async", "xtq_vit_status_dev", "xtq_vit_viterbi_dev",
-                   "xtq_ldlq_chain_dev",
+                   "xtq_ldlq_chain_dev", "xtq_ldlq_chain_multi_dev",
                    "xtq_trellis_decode_dev", "xtq_trellis_pack_dev",
                    "xtq_trellis_unpack_dev", "xtq_vit_get_lut"):
             getattr(L, fn).restype = i32
@@ -142,13 +144,19 @@ def status(device=None):
         _check("xtq_vit_status_dev", lib().xtq_vit_status_dev(_stream(dev)))
 
 
-def ldlq_chain(W: torch.Tensor, L: torch.Tensor | None, K: int, pivot: int, margin: int,
-               code: str = "mul1", states: bool = True, targets: bool = False):
+def ldlq_chain(W: torch.Tensor, L: torch.Tensor | None, K, pivot: int, margin: int,
+               code: str = "mul1", states: bool = True, targets: bool = False,
+               groups=None):
     """BlockLDLQ sweep of W [k, n] fp32 (inner domain, device) with the
     block-LDL factor L [k, k] (or None: no feedback) as column chains on the
     GPU (xtq_ldlq_chain_dev).  Returns (What [k, n] fp32, states int32
     [k/16, n/16, 256] or None, trellis int16 [k/16, n/16, 16K], targets fp32
-    [k/16, n/16, 256] or None), all on W's device."""
+    [k/16, n/16, 256] or None), all on W's device.
+
+    groups: None (all columns at K), or a list of (ncols, K) that splits W's
+    columns into consecutive groups encoded at their own K
+    (xtq_ldlq_chain_multi_dev); the trellis is then a list with one
+    [k/16, ncols/16, 16K] tensor per group."""
     W = _dev_tensor(W, torch.float32, "W")
     if W.dim() != 2 or W.shape[0] % 16 or W.shape[1] % 16:
         raise ValueError(f"W must be [k, n] with k, n multiples of 16, got {tuple(W.shape)}")
@@ -157,20 +165,31 @@ def ldlq_chain(W: torch.Tensor, L: torch.Tensor | None, K: int, pivot: int, marg
         L = _dev_tensor(L, torch.float32, "L")
         if L.shape != (k, k) or L.device != W.device:
             raise ValueError(f"L must be [{k}, {k}] on {W.device}")
+    single = groups is None
+    if single:
+        groups = [(n, int(K))]
+    groups = [(int(c), int(kk)) for c, kk in groups]
+    if sum(c for c, _ in groups) != n or any(c <= 0 or c % 16 for c, _ in groups):
+        raise ValueError(f"group widths {[c for c, _ in groups]} must be multiples of 16 "
+                         f"summing to {n}")
     tk, tn = k // 16, n // 16
     dev = W.device
     hatW = torch.empty(k, n, dtype=torch.float32, device=dev)
     st = torch.empty(tk, tn, 256, dtype=torch.int32, device=dev) if states else None
-    tr = torch.empty(tk, tn, 16 * K, dtype=torch.int16, device=dev)
+    trs = [torch.empty(tk, c // 16, 16 * kk, dtype=torch.int16, device=dev) for c, kk in groups]
     xt = torch.empty(tk, tn, 256, dtype=torch.float32, device=dev) if targets else None
+    ng = len(groups)
+    ncols = (ctypes.c_int * ng)(*[c for c, _ in groups])
+    ks = (ctypes.c_int * ng)(*[kk for _, kk in groups])
+    ptrs = (ctypes.c_void_p * ng)(*[t.data_ptr() for t in trs])
     with torch.cuda.device(dev):
-        rc = lib().xtq_ldlq_chain_dev(
-            W.data_ptr(), L.data_ptr() if L is not None else None, k, n, int(K),
+        rc = lib().xtq_ldlq_chain_multi_dev(
+            W.data_ptr(), L.data_ptr() if L is not None else None, k, n, ng, ncols, ks,
             code_name(code).encode(), int(margin), int(pivot), hatW.data_ptr(),
-            st.data_ptr() if st is not None else None, tr.data_ptr(),
+            st.data_ptr() if st is not None else None, ptrs,
             xt.data_ptr() if xt is not None else None, _stream(dev))
-    _check("xtq_ldlq_chain_dev", rc)
-    return hatW, st, tr, xt
+    _check("xtq_ldlq_chain_multi_dev", rc)
+    return hatW, st, (trs[0] if single else trs), xt
 
 
 def viterbi(X: torch.Tensor, K: int, overlap: torch.Tensor | None = None,

@@ -388,6 +388,7 @@ def ldlq_viterbi(Wq: torch.Tensor, Lfac: torch.Tensor | None, lut: torch.Tensor,
     feedback = Lfac is not None and bool(Lfac.any())
     tk, tn = k // 16, n // 16
     ldlq_viterbi.last_targets = None
+    ldlq_viterbi.last_groups = None
     if schedule == "chain":
         Wg = Wq.to(gdev, torch.float32).contiguous()
         Lg = Lfac.to(gdev, torch.float32).contiguous() if feedback else None
@@ -438,6 +439,7 @@ def ldlq_viterbi(Wq: torch.Tensor, Lfac: torch.Tensor | None, lut: torch.Tensor,
 
 ldlq_viterbi.last_trellis = None
 ldlq_viterbi.last_targets = None
+ldlq_viterbi.last_groups = None
 ldlq_viterbi.keep_targets = False
 
 
@@ -491,14 +493,16 @@ def quantize_linear(W: torch.Tensor, H_x: torch.Tensor | None, code: str = "exl3
 
 
 def quantize_linear_group(Ws, H_x: torch.Tensor | None, code: str = "exl3_mul1",
-                          K: int = 4, L: int = 16, V: int = 0, percdamp: float = 0.01,
+                          K=4, L: int = 16, V: int = 0, percdamp: float = 0.01,
                           su_seed: int = 20261011, buf_cols: int = 128,
                           use_ldlq: bool = True, device: str = "cpu",
                           batch: int = 0, dtype: torch.dtype = torch.float32,
                           margin: int = 0, compiled: bool = False, progress=None,
                           backend: str = "hip", channel_scales: bool = False):
     """quantize_linear for several weights that read the same input (one
-    H_x, e.g. the q/k/v or gate/up projections of a layer) at the same K.
+    H_x, e.g. the q/k/v or gate/up projections of a layer).  K is one bit
+    width for all members or one per member (mixed-K, e.g. q at 5 and k/v
+    at 7).
 
     The block-LDL factor is computed once and the members' inner weights are
     quantized side by side in one BlockLDLQ sweep: the sweep's feedback only
@@ -506,11 +510,16 @@ def quantize_linear_group(Ws, H_x: torch.Tensor | None, code: str = "exl3_mul1",
     the column-chain schedule (GPU tensors) every result is bit-identical to
     a separate quantize_linear call; narrow members (out/16 below the GPU's
     compute-unit count) then share the GPU instead of leaving most of it
-    idle.  Returns the list of quantize_linear result dicts, in order.
+    idle, and members of different K run as concurrent launches over a split
+    of the compute units.  Returns the list of quantize_linear result dicts,
+    in order.
     """
     Ws = list(Ws)
     if not Ws:
         raise ValueError("quantize_linear_group needs at least one weight")
+    Ks = [int(K)] * len(Ws) if isinstance(K, int) else [int(x) for x in K]
+    if len(Ks) != len(Ws):
+        raise ValueError(f"{len(Ks)} bit widths for {len(Ws)} weights")
     k_in = Ws[0].shape[1]
     for W in Ws:
         if W.dim() != 2 or W.shape[1] != k_in:
@@ -567,23 +576,69 @@ def quantize_linear_group(Ws, H_x: torch.Tensor | None, code: str = "exl3_mul1",
         if progress is not None:
             progress("hinv", time.time() - t0)
 
-    hatWq, states = ldlq_viterbi(Wq, Lfac, lut, K, L, buf_cols=buf_cols, V=V,
-                                 batch=batch, dtype=dtype, margin=margin,
-                                 compiled=compiled, progress=progress,
-                                 code=code, backend=backend)
-    trellis = ldlq_viterbi.last_trellis                          # GPU
+    # runs of consecutive members with the same K: (first column, columns, K)
+    runs = []
+    for mb, Km in zip(members, Ks):
+        if runs and runs[-1][2] == Km:
+            runs[-1][1] += mb["n"]
+        else:
+            runs.append([sum(r[1] for r in runs), mb["n"], Km])
+    sched = DEFAULT_SCHEDULE if DEFAULT_SCHEDULE != "auto" else \
+        ("chain" if Wq.is_cuda else "block")
+    if len(runs) == 1:
+        hatWq, states = ldlq_viterbi(Wq, Lfac, lut, Ks[0], L, buf_cols=buf_cols, V=V,
+                                     batch=batch, dtype=dtype, margin=margin,
+                                     compiled=compiled, progress=progress,
+                                     code=code, backend=backend)
+        run_tr = [ldlq_viterbi.last_trellis]                      # GPU
+    elif sched == "chain":
+        # one call: a concurrent chain launch per run (xtq_ldlq_chain_multi_dev)
+        _check_viterbi_args(L, V, dtype, "sq")
+        gdev = _on_gpu(torch.empty(0)).device if not Wq.is_cuda else Wq.device
+        feedback = Lfac is not None and bool(Lfac.any())
+        hatWq, st, run_tr, xt = _hb.ldlq_chain(
+            Wq.to(gdev, torch.float32).contiguous(),
+            Lfac.to(gdev, torch.float32).contiguous() if feedback else None, None, 128,
+            int(margin), code=_hb.code_name(_kernel_code(lut, L)), states=True,
+            targets=bool(ldlq_viterbi.keep_targets), groups=[(r[1], r[2]) for r in runs])
+        states = st.long().to(dev)
+        hatWq = hatWq.to(dev)
+        ldlq_viterbi.last_targets = xt
+        ldlq_viterbi.last_trellis = None
+        ldlq_viterbi.last_groups = [(r[0], r[1], r[2], t) for r, t in zip(runs, run_tr)]
+        if progress is not None:
+            progress(0, 512 * (Wq.shape[0] // 16))
+    else:
+        hatWq = torch.empty_like(Wq)
+        states = torch.empty(Wq.shape[0] // 16, Wq.shape[1] // 16, 256, dtype=torch.long,
+                             device=dev)
+        run_tr = []
+        for c0, nc, Kr in runs:
+            hw, stv = ldlq_viterbi(Wq[:, c0:c0 + nc].contiguous(), Lfac, lut, Kr, L,
+                                   buf_cols=buf_cols, V=V, batch=batch, dtype=dtype,
+                                   margin=margin, compiled=compiled, progress=progress,
+                                   code=code, backend=backend)
+            hatWq[:, c0:c0 + nc] = hw
+            states[:, c0 // 16:(c0 + nc) // 16] = stv
+            run_tr.append(ldlq_viterbi.last_trellis)
     # bit-exact self-checks of the format round trip (quantize.py:848-853),
-    # compared where the trellis lives
-    st_rt = _hb.unpack(trellis.view(-1, 16 * K), K)
-    assert torch.equal(st_rt, states.reshape(-1, 256).to(st_rt.device, torch.int32)), \
-        "pack/unpack round-trip broke state sequence"
-    hatW_g = _hb.decode(trellis, K, code=_hb.code_name(code))
-    assert torch.equal(hatW_g, hatWq.to(hatW_g.device)), "decode != encoder output"
+    # compared where the trellis lives, per run of one K
+    hatW_parts = []
+    for (c0, nc, Kr), trellis in zip(runs, run_tr):
+        st_rt = _hb.unpack(trellis.view(-1, 16 * Kr), Kr)
+        st_ref = states[:, c0 // 16:(c0 + nc) // 16].reshape(-1, 256)
+        assert torch.equal(st_rt, st_ref.to(st_rt.device, torch.int32)), \
+            "pack/unpack round-trip broke state sequence"
+        hw = _hb.decode(trellis, Kr, code=_hb.code_name(code))
+        assert torch.equal(hw, hatWq[:, c0:c0 + nc].to(hw.device)), "decode != encoder output"
+        hatW_parts.append(hw)
     out, off = [], 0
-    for mb in members:
+    for mb, Km in zip(members, Ks):
         n = mb["n"]
-        hatW_d = hatW_g[:, off:off + n].contiguous().to(dev)
-        tr = trellis[:, off // 16:(off + n) // 16].contiguous()
+        ri = max(i for i, r in enumerate(runs) if r[0] <= off)
+        c0 = off - runs[ri][0]
+        hatW_d = hatW_parts[ri][:, c0:c0 + n].contiguous().to(dev)
+        tr = run_tr[ri][:, c0 // 16:(c0 + n) // 16].contiguous()
         off += n
         Wscale, suh, svh = mb["Wscale"], mb["suh"], mb["svh"]
         if channel_scales:
@@ -597,7 +652,7 @@ def quantize_linear_group(Ws, H_x: torch.Tensor | None, code: str = "exl3_mul1",
             "trellis": _to_host(tr),
             "suh": suh.cpu(), "svh": svh.cpu(),
             "Wscale": float(Wscale), "lut_rms": float(lut_rms),
-            "code": code, "K": K, "L": L, "V": V, "use_ldlq": use_ldlq,
+            "code": code, "K": Km, "L": L, "V": V, "use_ldlq": use_ldlq,
             "channel_scales": channel_scales,
         })
     return out

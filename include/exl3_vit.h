@@ -149,6 +149,22 @@ XTQ_API int xtq_ldlq_chain_dev(const float* d_W, const float* d_L, int k, int n,
                                void* stream);
 
 /*
+ * xtq_ldlq_chain_dev for weights quantized side by side at different K
+ * (e.g. a layer's q/k/v projections, which share one input Hessian): W's
+ * columns are ngroups consecutive groups of h_ncols[g] columns (multiples
+ * of 16, summing to n) encoded at h_K[g] bits, group g's trellis going to
+ * h_trellis[g] ([k/16][h_ncols[g]/16][16 h_K[g]] int16 device).  The groups
+ * run as concurrent launches over a split of the compute units; every tile
+ * encodes exactly as in a single-group call.  No reference counterpart (the
+ * reference quantizes one weight at a time).  At most 8 groups.
+ */
+XTQ_API int xtq_ldlq_chain_multi_dev(const float* d_W, const float* d_L, int k, int n,
+                                     int ngroups, const int* h_ncols, const int* h_K,
+                                     const char* code, int margin, int pivot, float* d_hatW,
+                                     int32_t* d_states, int16_t* const* h_trellis,
+                                     float* d_targets, void* stream);
+
+/*
  * Device-pointer single Viterbi run: the HIP counterpart of viterbi()
  * (quantize.py:218-320) with V = 1 and L = 16.
  *   dX         [nseq][T] fp32 device, 1 <= T <= 256

@@ -82,6 +82,18 @@ def test_status_codes_without_device(lib):
     assert ch(fake, mis, 64, 64, 4, b"mul1", 0, 128, fake, None, fake, None, None) == 12
     assert ch(fake, fake, 72, 64, 4, b"mul1", 0, 128, fake, None, fake, None, None) == 6
     assert ch(fake, None, 64, 0, 4, b"mul1", 0, 128, fake, None, fake, None, None) == 6
+    chm = lib.xtq_ldlq_chain_multi_dev
+    i2 = (ctypes.c_int * 2)
+    tp2 = (ctypes.c_void_p * 2)(16, 16)
+    tp1 = (ctypes.c_void_p * 2)(16, None)
+    args = (b"mul1", 0, 128, fake, None)
+    assert chm(fake, None, 64, 64, 2, i2(32, 32), i2(4, 9), *args, tp2, None, None) == 9
+    assert chm(fake, None, 64, 64, 2, i2(32, 24), i2(4, 7), *args, tp2, None, None) == 6
+    assert chm(fake, None, 64, 64, 2, i2(32, 16), i2(4, 7), *args, tp2, None, None) == 6
+    assert chm(fake, None, 64, 64, 0, i2(64, 0), i2(4, 7), *args, tp2, None, None) == 6
+    assert chm(fake, None, 64, 64, 9, i2(32, 32), i2(4, 7), *args, tp2, None, None) == 6
+    assert chm(fake, None, 64, 64, 2, i2(32, 32), i2(4, 7), *args, tp1, None, None) == 12
+    assert chm(fake, None, 64, 64, 2, None, i2(4, 7), *args, tp2, None, None) == 12
     out = ctypes.c_double()
     assert lib.xtq_valu_probe(7, ctypes.byref(out)) == 8
     assert lib.xtq_valu_probe(0, None) == 12

@@ -217,3 +217,49 @@ def test_to_host_staging(xq):
         h = xq._to_host(t.view(-1, 1) if n % 2 else t.view(2, -1))
         assert h.device.type == "cpu" and not h.is_pinned()
         assert torch.equal(h.view(-1), t.cpu())
+
+
+@pytest.mark.parametrize("Ks,device", [((5, 7, 7), "cuda"), ((4, 6, 4), "cuda"),
+                                       ((3, 6), "cpu")])
+def test_quantize_linear_group_mixed_k(xq, Ks, device):
+    """Members at different K in one call (concurrent chain launches over a
+    split of the CUs on the GPU; one block sweep per K run on the CPU) give
+    exactly the results of separate quantize_linear calls."""
+    import workloads as wl
+    g = torch.Generator().manual_seed(13)
+    H = wl.ar1_gram(256, 512, 0.4, 13)
+    rows = (256, 128, 128)
+    Ws = [0.02 * torch.randn(rows[m], 256, generator=g) for m in range(len(Ks))]
+    print(f"case quantize_linear_group K={Ks} on {device}", flush=True)
+    grp = xq.quantize_linear_group(Ws, H, K=list(Ks), device=device, channel_scales=True)
+    for W, Km, r in zip(Ws, Ks, grp):
+        s = xq.quantize_linear(W, H, K=Km, device=device, channel_scales=True)
+        assert r["K"] == Km and r["trellis"].shape == (16, W.shape[0] // 16, 16 * Km)
+        for key in ("W_hat", "trellis", "suh", "svh"):
+            assert torch.equal(r[key], s[key]), (Km, key)
+
+
+def test_chain_groups_match_single_launches(hb, oracle_mod, mul1_lut):
+    """hb.ldlq_chain over column groups of different K equals single-K calls
+    on each group's columns (tiles of one column never see another's), and
+    the concurrent launches encode every tile as the oracle does."""
+    g = torch.Generator().manual_seed(14)
+    k = 128
+    W = torch.randn(k, 96, generator=g)
+    L = torch.tril(0.05 * torch.randn(k, k, generator=g), -16).contiguous()
+    groups = [(32, 3), (48, 7), (16, 5)]
+    print("case chain groups 128x96 K=3/7/5", flush=True)
+    hatW, st, trs, xt = hb.ldlq_chain(W.cuda(), L.cuda(), None, 128, 0, targets=True,
+                                      groups=groups)
+    c0 = 0
+    for (nc, K), tr in zip(groups, trs):
+        h1, s1, t1, x1 = hb.ldlq_chain(W[:, c0:c0 + nc].contiguous().cuda(), L.cuda(), K, 128,
+                                       0, targets=True)
+        assert torch.equal(hatW[:, c0:c0 + nc], h1)
+        assert torch.equal(st[:, c0 // 16:(c0 + nc) // 16], s1)
+        assert torch.equal(tr, t1)
+        assert torch.equal(xt[:, c0 // 16:(c0 + nc) // 16], x1)
+        want = oracle_mod.tailbite(x1.reshape(-1, 256).cpu().numpy(), mul1_lut, K, 16,
+                                   pivot=128, margin=0, nthreads=8)
+        np.testing.assert_array_equal(s1.reshape(-1, 256).cpu().numpy(), want)
+        c0 += nc
