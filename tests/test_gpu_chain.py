@@ -263,3 +263,36 @@ def test_chain_groups_match_single_launches(hb, oracle_mod, mul1_lut):
                                    pivot=128, margin=0, nthreads=8)
         np.testing.assert_array_equal(s1.reshape(-1, 256).cpu().numpy(), want)
         c0 += nc
+
+
+@pytest.mark.parametrize("k,n,K,pivot,margin", [(16, 64, 4, 128, 0), (32, 16, 6, 250, 16),
+                                                (48, 32, 2, 0, 255)])
+def test_chain_edge_shapes(xq, hb, oracle_mod, mul1_lut, k, n, K, pivot, margin):
+    """One block row (no feedback at all), one column, and margins where
+    pivot + margin reaches the end of the sequence (pass 1 runs 256 steps)."""
+    g = torch.Generator().manual_seed(15 + k + n)
+    W = torch.randn(k, n, generator=g)
+    L = torch.tril(0.1 * torch.randn(k, k, generator=g), -16).contiguous()
+    print(f"case chain edge {k}x{n} K={K} pivot={pivot} margin={margin}", flush=True)
+    hatW, st, tr, xt = (t.cpu() for t in hb.ldlq_chain(W.cuda(), L.cuda(), K, pivot, margin,
+                                                        targets=True))
+    _check_targets(W, L, hatW, xt, xq.tensor_core_perm())
+    _check_tiles(oracle_mod, mul1_lut, K, pivot, margin, st, tr, xt)
+
+
+def test_chain_many_groups(hb):
+    """Four column groups (one narrower than its share of the CUs) equal
+    single-K launches over their columns."""
+    g = torch.Generator().manual_seed(16)
+    k = 96
+    W = torch.randn(k, 192, generator=g).cuda()
+    L = torch.tril(0.05 * torch.randn(k, k, generator=g), -16).contiguous().cuda()
+    groups = [(16, 2), (96, 4), (32, 6), (48, 7)]
+    print("case chain 4 groups", flush=True)
+    hatW, st, trs, _ = hb.ldlq_chain(W, L, None, 147, 16, groups=groups)
+    c0 = 0
+    for (nc, K), tr in zip(groups, trs):
+        h1, s1, t1, _ = hb.ldlq_chain(W[:, c0:c0 + nc].contiguous(), L, K, 147, 16)
+        assert torch.equal(hatW[:, c0:c0 + nc], h1) and torch.equal(tr, t1)
+        assert torch.equal(st[:, c0 // 16:(c0 + nc) // 16], s1)
+        c0 += nc
