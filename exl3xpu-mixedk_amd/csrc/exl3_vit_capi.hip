@@ -445,7 +445,8 @@ double chain_tile_cost(int K) {
 // column chain, at least one, summing to at most ncu.
 void split_cus(int ncu, int ng, const int* tng, const int* Kg, int tk, int* nwg) {
     if (ng == 1) {
-        nwg[0] = ncu;
+        // more workgroups than column chains could only wait
+        nwg[0] = tng[0] < ncu ? tng[0] : ncu;
         return;
     }
     double w[kMaxChainGroups], tot = 0.0;
