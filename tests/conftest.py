@@ -36,3 +36,14 @@ def oracle_mod():
 @pytest.fixture(scope="session")
 def mul1_lut(oracle_mod):
     return oracle_mod.code_lut("exl3_mul1")
+
+
+@pytest.fixture()
+def cpu8():
+    """8 torch CPU threads: the end-to-end golden vectors were written with 8,
+    and CPU reductions round by their thread split."""
+    import torch
+    prev = torch.get_num_threads()
+    torch.set_num_threads(8)
+    yield
+    torch.set_num_threads(prev)

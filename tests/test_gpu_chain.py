@@ -296,3 +296,63 @@ def test_chain_many_groups(hb):
         assert torch.equal(hatW[:, c0:c0 + nc], h1) and torch.equal(tr, t1)
         assert torch.equal(st[:, c0 // 16:(c0 + nc) // 16], s1)
         c0 += nc
+
+
+def test_chain_targets_vs_golden_pinned_block_path(xq, hb, monkeypatch, cpu8):
+    """The reference's own 128x128 AR(1) case: the block schedule with the
+    torch work on the CPU reproduces the reference's golden trellis bit for
+    bit, so its per-launch targets are the reference's.  The chain, fed the
+    same inner weights and factor, must produce those targets within the
+    fp32 rounding of the two summation orders wherever the tiles below in the
+    column encoded identically (so E agrees), and exactly W for the first
+    block row swept."""
+    from conftest import load_golden
+    e = load_golden("e2e_128.npz")
+    W, H = torch.from_numpy(e["W"]), torch.from_numpy(e["H_ar"])
+    seen, launches = {}, []
+    real_ldlq, real_launch = xq.ldlq_viterbi, xq._launch
+
+    def rec_ldlq(Wq, Lfac, *a, **kw):
+        seen["Wq"], seen["Lfac"] = Wq.clone(), Lfac.clone()
+        return real_ldlq(Wq, Lfac, *a, **kw)
+
+    def rec_launch(X, K, code, pivot, margin):
+        launches.append(X.detach().cpu().clone())
+        return real_launch(X, K, code, pivot, margin)
+
+    monkeypatch.setattr(xq, "DEFAULT_SCHEDULE", "block")
+    monkeypatch.setattr(xq, "_launch", rec_launch)
+    monkeypatch.setattr(xq, "ldlq_viterbi", rec_ldlq)
+    xq.ldlq_viterbi.last_trellis = None
+    print("case golden 128x128 AR(1): block schedule on the CPU", flush=True)
+    r = xq.quantize_linear(W, H, code="exl3_mul1", K=4, use_ldlq=True, margin=0, device="cpu")
+    np.testing.assert_array_equal(r["trellis"].numpy(), e["ar_trellis"])      # pinned
+    Wq, Lf = seen["Wq"], seen["Lfac"]
+    k, n = Wq.shape
+    tk, tn = k // 16, n // 16
+    Xb = torch.stack(launches[::-1])                       # [tk, tn, 256], block i first
+    print("case golden 128x128 AR(1): chain on the GPU", flush=True)
+    hatW, st, tr, xt = (t.cpu() for t in hb.ldlq_chain(Wq.cuda(), Lf.cuda(), 4, 128, 0,
+                                                        targets=True))
+    perm = xq.tensor_core_perm()
+    assert torch.equal(xt[tk - 1], Xb[tk - 1])            # no feedback: exactly W
+    same = (tr == torch.from_numpy(e["ar_trellis"])).all(dim=-1)              # [tk, tn]
+    # |x_chain - x_block| <= (k/4 + 36 + k) u (|W| + sum |L| |E|)
+    E = (Wq - hatW).double()
+    B = Wq.double().abs()
+    L64 = Lf.double()
+    for i in range(tk - 1):
+        B[16 * i:16 * (i + 1)] += L64[16 * (i + 1):, 16 * i:16 * (i + 1)].abs().t() @ \
+            E[16 * (i + 1):].abs()
+    lim = (k / 4 + 36 + k) * U32 * _seq_order(B, perm)
+    checked = 0
+    for j in range(tn):
+        for i in range(tk - 2, -1, -1):
+            if not bool(same[i + 1:, j].all()):
+                break
+            d = (xt[i, j].double() - Xb[i, j].double()).abs()
+            assert bool((d <= lim[i, j]).all()), (i, j, float((d - lim[i, j]).max()))
+            checked += 1
+    print(f"tiles identical to the golden trellis: {int(same.sum())}/{tk * tn}, "
+          f"targets checked: {checked}")
+    assert checked >= (tk - 1) * tn // 2

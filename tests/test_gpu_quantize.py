@@ -25,14 +25,6 @@ def xq():
     return quantize
 
 
-@pytest.fixture()
-def cpu8():
-    prev = torch.get_num_threads()
-    torch.set_num_threads(8)           # the fixtures were written with 8 threads
-    yield
-    torch.set_num_threads(prev)
-
-
 @pytest.mark.parametrize("tag,ldlq,cs", [("id", True, False), ("ar", True, False),
                                          ("arcs", True, True), ("nold", False, False)])
 def test_quantize_linear_golden(xq, cpu8, tag, ldlq, cs):
