@@ -773,7 +773,7 @@ __global__ __launch_bounds__(64) void pack_kernel(const int32_t* __restrict__ st
 // so tile (i, j) depends only on tile (i+1, j): the columns are independent
 // chains.  Each of the persistent workgroups takes tile tasks from an atomic
 // counter in sweep order (block tk-1 first), waits (acquire, bounded) for
-// the tile above in its column, computes the targets (the L and E column
+// the previous tile of its chain, (i+1, j), computes the targets (the L and E column
 // blocks read in the matrix-core operand layout described below), runs
 // both tail-biting passes with in-workgroup tracebacks,
 // writes the states, the packed trellis, What and E for the tile, and
@@ -864,7 +864,7 @@ __global__ __launch_bounds__(kFwdThreads) void ldlq_chain_kernel(
         const int i = tk - 1 - t / tnl, jl = t - (t / tnl) * tnl, j = jc0 + jl;
         // targets row: the workgroup's own, or the tile's (row-block order)
         float* const xs = xbuf + (xdump ? (size_t)i * tn + j : (size_t)blockIdx.x) * kSteps;
-        // wait for tile (i+1, j) (task t - tn)
+        // wait for tile (i+1, j), this launch's task t - tnl
         if (tid == 0) {
             int good = 1;
             if (Lq != nullptr && i + 1 < tk) {
