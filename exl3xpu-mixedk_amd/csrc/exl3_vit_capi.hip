@@ -321,7 +321,7 @@ int pick_group(const DevCtx& cx, int K, int n) {
         // to what the LDS footprint for K allows.
         const int want = atoi(g);
         const int cap = xtq::forward_group(K, 1 << 30, 1);
-        if (want == 1 || want == 2 || want == 4) T = want < cap ? want : cap;
+        if (want == 1 || want == 2 || want == 4 || want == 8) T = want < cap ? want : cap;
     }
     return T;
 }

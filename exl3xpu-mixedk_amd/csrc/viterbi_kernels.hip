@@ -190,14 +190,17 @@ __device__ __forceinline__ void fwd_run(
     auto& ovs = sm.ovs;
     auto& red = sm.red;
 
-    if (tid < T * kSteps) {
-        const int tt = tid / kSteps, e = tid % kSteps;
-        float v = 0.0f;
-        if (tt < ntile && e < xlen) {
-            v = X[(size_t)(q0 + tt) * xstride + e];
-            if (v != v) atomicOr(err, 1u);
+#pragma unroll
+    for (int r0 = 0; r0 < T * kSteps; r0 += kFwdThreads) {
+        if (r0 + kFwdThreads <= T * kSteps || tid < T * kSteps - r0) {
+            const int idx = r0 + tid, tt = idx / kSteps, e = idx % kSteps;
+            float v = 0.0f;
+            if (tt < ntile && e < xlen) {
+                v = X[(size_t)(q0 + tt) * xstride + e];
+                if (v != v) atomicOr(err, 1u);
+            }
+            xs[tt][e] = v;
         }
-        xs[tt][e] = v;
     }
 
     // Owned groups and candidates: groups j_c = jbase + c, candidate w of a
@@ -1027,7 +1030,8 @@ hipError_t dispatch_k(int K, A... a) {
 template <int K>
 constexpr int max_group() {
     constexpr size_t per = 2 * sizeof(float) * Geom<K>::SPL + 1024 + 16;
-    return (4 * per + 512 <= 160 * 1024) ? 4 : (2 * per + 512 <= 160 * 1024) ? 2 : 1;
+    return (8 * per + 512 <= 160 * 1024) ? 8 : (4 * per + 512 <= 160 * 1024) ? 4
+         : (2 * per + 512 <= 160 * 1024) ? 2 : 1;
 }
 
 template <int K>
@@ -1036,7 +1040,7 @@ struct FwdL {
                           const uint16_t* lut16, int roll, int nsteps, int store_lo,
                           const int32_t* ov_in, void* bp, int32_t* send, uint32_t* err,
                           int group, hipStream_t s) {
-        const int T = group <= 1 ? 1 : group <= 2 ? 2 : 4;
+        const int T = group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 ? 4 : 8;
         if (T > max_group<K>()) return hipErrorInvalidValue;
         const int nwg = (nseq + T - 1) / T;
         if (T == 1)
@@ -1049,11 +1053,16 @@ struct FwdL {
                                    X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo,
                                    ov_in,
                                    (uint8_t*)bp, send, err, 1.0f);
-            else if constexpr (max_group<K>() >= 4)
-                hipLaunchKernelGGL((fwd_kernel<K, 4>), dim3(nwg), dim3(kFwdThreads), 0, s,
-                                   X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo,
-                                   ov_in,
-                                   (uint8_t*)bp, send, err, 1.0f);
+            else if constexpr (max_group<K>() >= 4) {
+                if (T == 4)
+                    hipLaunchKernelGGL((fwd_kernel<K, 4>), dim3(nwg), dim3(kFwdThreads), 0, s,
+                                       X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo,
+                                       ov_in, (uint8_t*)bp, send, err, 1.0f);
+                else if constexpr (max_group<K>() >= 8)
+                    hipLaunchKernelGGL((fwd_kernel<K, 8>), dim3(nwg), dim3(kFwdThreads), 0, s,
+                                       X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo,
+                                       ov_in, (uint8_t*)bp, send, err, 1.0f);
+            }
         }
         return hipGetLastError();
     }

@@ -85,10 +85,10 @@ def test_short_runs_vs_oracle(hb, oracle_mod, mul1_lut, K):
 
 
 @pytest.mark.parametrize("K", range(2, 8))
-@pytest.mark.parametrize("group", ["1", "2", "4", "fused"])
+@pytest.mark.parametrize("group", ["1", "2", "4", "8", "fused"])
 def test_oracle_random(hb, oracle_mod, mul1_lut, K, group, monkeypatch):
     """Random Gaussian and tie-heavy batches against the oracle, with each
-    code path forced: separate pass launches at 1, 2 or 4 sequences per
+    code path forced: separate pass launches at 1, 2, 4 or 8 sequences per
     workgroup, or the fused two-pass launch; odd batch sizes included."""
     if group == "fused":
         monkeypatch.setenv("XTQ_VIT_FUSED", "1")
