@@ -786,8 +786,7 @@ int xtq_ldlq_chain_multi_dev(const float* d_W, const float* d_L, int k, int n, i
     if (pivot < 0 || pivot >= xtq::kSteps || margin < 0) return 10;
     if (d_L && ((uintptr_t)d_L & 15)) return 12;     // rows are read as float4
     if (k <= 0 || n <= 0 || k % 16 || n % 16 || col != n ||
-        (long long)(k / 16) * (n / 16) > g_maxseq || (long long)k * n > (1LL << 31) - 1 ||
-        (long long)k * k > (1LL << 31) - 1)
+        (long long)(k / 16) * (n / 16) > g_maxseq || k > (1 << 22))
         return 6;
     int dev = 0;
     if (current_device(&dev)) return 1;

@@ -356,3 +356,30 @@ def test_chain_targets_vs_golden_pinned_block_path(xq, hb, monkeypatch, cpu8):
     print(f"tiles identical to the golden trellis: {int(same.sum())}/{tk * tn}, "
           f"targets checked: {checked}")
     assert checked >= (tk - 1) * tn // 2
+
+
+def test_chain_factor_over_2g_elements(hb, oracle_mod, mul1_lut):
+    """k = 46400: the block-LDL factor holds more than 2^31 elements (8.6 GB),
+    so every index into it and into E must be 64-bit; one column chain of
+    2,900 tiles.  Targets of tiles spread over the sweep against the fp64
+    formula on the kernel's own What, and their encodes against the oracle."""
+    k, n = 46400, 16
+    assert k * k > 2 ** 31
+    g = torch.Generator(device="cuda").manual_seed(17)
+    W = torch.randn(k, n, device="cuda", generator=g)
+    L = torch.randn(k, k, device="cuda", generator=g).mul_(0.002).tril_(-16)
+    print("case chain k=46400 n=16 K=4", flush=True)
+    hatW, st, tr, xt = hb.ldlq_chain(W, L, 4, 128, 0, targets=True)
+    perm = torch.tensor(oracle_mod.tensor_core_perm(), device="cuda", dtype=torch.long)
+    E = (W - hatW).double()
+    tk = k // 16
+    for i in (0, 1, tk // 2, tk - 2, tk - 1):
+        r0, r1 = 16 * i, 16 * (i + 1)
+        X64 = W[r0:r1].double() + L[r1:, r0:r1].double().t() @ E[r1:]
+        B = W[r0:r1].double().abs() + L[r1:, r0:r1].double().abs().t() @ E[r1:].abs()
+        x64 = X64.reshape(-1)[perm]
+        lim = (k / 4 + 36) * U32 * B.reshape(-1)[perm]
+        assert bool(((xt[i, 0].double() - x64).abs() <= lim).all()), i
+        want = oracle_mod.tailbite(xt[i].cpu().numpy(), mul1_lut, 4, 16, pivot=128, margin=0)
+        np.testing.assert_array_equal(st[i].cpu().numpy(), want)
+    del L
