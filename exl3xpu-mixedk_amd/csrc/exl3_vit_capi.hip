@@ -317,7 +317,7 @@ int finish(DevCtx& cx, hipStream_t s) {
 int pick_group(const DevCtx& cx, int K, int n) {
     int T = xtq::forward_group(K, n, cx.ncu);
     if (const char* g = getenv("XTQ_VIT_GROUP")) {
-        // Test hook: force the sequences per workgroup (1, 2 or 4), clamped
+        // Test hook: force the sequences per workgroup (1, 2, 4 or 8), clamped
         // to what the LDS footprint for K allows.
         const int want = atoi(g);
         const int cap = xtq::forward_group(K, 1 << 30, 1);

@@ -9,7 +9,7 @@
 
 namespace xtq {
 
-// Threads per forward workgroup; one workgroup advances T (1, 2 or 4)
+// Threads per forward workgroup; one workgroup advances T (1, 2, 4 or 8)
 // 256-step sequences in lockstep, 64 trellis states per thread per sequence.
 constexpr int kFwdThreads = 1024;
 // Threads per traceback workgroup.

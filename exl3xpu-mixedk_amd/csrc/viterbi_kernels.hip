@@ -10,7 +10,7 @@
 // Work decomposition (16-bit state, K bits per step, NC = 2^K predecessors,
 // SP = 2^(16-K) groups):
 //   * one 1024-thread workgroup (16 waves, one per CU at 4 waves/SIMD)
-//     advances T = 1, 2 or 4 sequences in lockstep;
+//     advances T = 1, 2, 4 or 8 sequences in lockstep;
 //   * thread t owns the C = SP/1024 consecutive groups j = t*C .. t*C+C-1
 //     (K=7: half of group t/2) and the candidate states of each,
 //     s = j + w*SP, i.e. 64 states per thread for every K; their codebook

@@ -38,7 +38,7 @@
  *   XTQ_VIT_MAXBYTES upper bound on library-owned device bytes (default 64 GiB)
  *   XTQ_VIT_SCRATCH  backpointer scratch budget in bytes; larger batches are
  *                    processed in chunks (default 8 GiB)
- *   XTQ_VIT_GROUP    force 1, 2 or 4 sequences per forward workgroup
+ *   XTQ_VIT_GROUP    force 1, 2, 4 or 8 sequences per forward workgroup
  *                    (testing; default chosen from the batch size)
  *   XTQ_VIT_TB_LANES smallest batch whose tracebacks run one lane per sequence
  *                    (0: always, -1: never; default 2048)
