@@ -292,3 +292,24 @@ def test_other_codebooks(hb, oracle_mod):
         Xd = torch.from_numpy(X).cuda()
         st, _ = hb.tailbite(Xd, 3, 128, 0, code=short)
         np.testing.assert_array_equal(st.cpu().numpy(), want)
+
+
+def test_verify_viterbi_readme_case(hb, oracle_mod, mul1_lut):
+    """The reference's kernel-tier check (verify_viterbi.py:20-65) on its
+    README case (seed 1, 64 sequences, code mul1, margin 0, pivot 128,
+    README.md:181-185), through the drop-in host entry xtq_vit_run: every
+    sequence exact (the reference passes at >= 99 %), decoded MSE equal, every
+    sequence circular-consistent."""
+    import ctypes
+    nseq = 64
+    X = np.random.default_rng(1).standard_normal((nseq, 256), dtype=np.float32)
+    out = np.empty((nseq, 256), dtype=np.int32)
+    rc = hb.lib().xtq_vit_run(X.ctypes.data_as(ctypes.c_void_p), nseq, b"mul1", 0, 128,
+                              out.ctypes.data_as(ctypes.c_void_p))
+    assert rc == 0
+    ref = oracle_mod.tailbite(X, mul1_lut, 4, 16, pivot=128, margin=0)
+    assert int((out == ref).all(axis=1).sum()) == nseq
+    mse_k = float(((mul1_lut[out] - X) ** 2).mean())
+    mse_r = float(((mul1_lut[ref] - X) ** 2).mean())
+    assert mse_k == mse_r
+    assert int(((out[:, 0] >> 4) == (out[:, -1] & ((1 << 12) - 1))).sum()) == nseq
