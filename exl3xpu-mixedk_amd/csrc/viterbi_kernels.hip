@@ -432,6 +432,66 @@ __global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
 }
 
 // ---------------------------------------------------------------- traceback
+// The links of slots hi down to lo of one staged chunk (slot sl's row at
+// stage + (sl - lo) * BPSTEP), chased by one thread from s = s_{hi+1}:
+// s_sl = x + bp_sl[x] * SP with x = s_{sl+1} >> K.  Returns s_lo; stores
+// st[sl] = s_sl when STORE.
+//
+// Written for the latency of the serial chain.  Each link reads the aligned
+// 32-bit word holding group x's bits (GW groups per word) and extracts them;
+// x_{sl-1} = x >> K | bp << (16 - 2K), so the next word's address is one
+// shift-add of bp onto a part that depends on x alone (the bit ranges are
+// disjoint), and wait -> extract -> shift-add -> load is the only dependent
+// path.  The state, its store, the next x and the next word's x part are
+// computed while the next load is in flight (the load after the last link
+// re-reads row 0).  The values live in VGPRs: a scalar chain pays a
+// readfirstlane per link.
+template <int K, bool STORE>
+__device__ __forceinline__ int chase_links(const uint8_t* stage, int hi, int lo, int32_t* st,
+                                           int s) {
+    using G = Geom<K>;
+    constexpr int LC = G::HALF ? 0 : 6 - K;                 // log2 groups per unit
+    constexpr int LUW = G::UNIT == 4 ? 0 : G::UNIT == 2 ? 1 : 2;  // log2 units per word
+    constexpr int LGW = LC + LUW;                           // log2 groups per word
+    constexpr int SB = 16 - 2 * K - LGW + 2;                // bp's shift in the next address
+    static_assert(16 - 2 * K >= LGW, "bp bits above the word index's x part");
+    // bit offset of group x in its word
+    auto offset = [](uint32_t x) {
+        return (x & ((1u << LC) - 1)) * K + ((x >> LC) & ((1u << LUW) - 1)) * (8 * G::UNIT);
+    };
+    int zero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+    uint32_t x = (uint32_t)((s + zero) >> K) & (uint32_t)(G::SP - 1);
+    uint32_t row = (uint32_t)(hi - lo) * G::BPSTEP;
+    uint32_t v = *(const uint32_t*)(stage + row + ((x >> LGW) << 2));
+    uint32_t sv = (uint32_t)s;
+    row = row >= (uint32_t)G::BPSTEP ? row - G::BPSTEP : 0u;
+    uint32_t rest = row + ((x >> (K + LGW)) << 2);
+    uint32_t sh = offset(x);
+    for (int sl = hi; sl >= lo; --sl) {
+        const uint32_t b = __builtin_amdgcn_ubfe(v, sh, (uint32_t)K);
+        uint32_t addr;
+        asm("v_lshl_add_u32 %0, %1, %2, %3" : "=v"(addr) : "v"(b), "i"(SB), "v"(rest));
+        v = *(const uint32_t*)(stage + addr);
+        __builtin_amdgcn_sched_barrier(0);   // the link's ops stay ahead of the rest
+        sv = x | (b << (16 - K));
+        if constexpr (STORE) st[sl] = (int32_t)sv;
+        x = (x >> K) | (b << (16 - 2 * K));
+        row = row >= (uint32_t)G::BPSTEP ? row - G::BPSTEP : 0u;
+        rest = row + ((x >> (K + LGW)) << 2);
+        sh = offset(x);
+    }
+    return (int)sv;
+}
+
+// The links of slots hi .. lo, storing the states when st is non-null.
+template <int K>
+__device__ __forceinline__ int chase_links(const uint8_t* stage, int hi, int lo, int32_t* st,
+                                           int s) {
+    return st ? chase_links<K, true>(stage, hi, lo, st, s)
+              : chase_links<K, false>(stage, hi, lo, st, s);
+}
+
 // Traceback of one sequence by the calling workgroup: from cur = s_{nsteps-1}
 // (shared; set by the caller before a barrier) down to step `stop`.  The
 // backpointer slots stop .. nsteps-2 (slot i-1 links s_i to s_{i-1}) are
@@ -452,16 +512,7 @@ __device__ __forceinline__ void tb_chase(const uint8_t* __restrict__ bpq, int ns
         __syncthreads();
         for (int k = tid; k < n16; k += nthr) stage[k] = src[k];
         __syncthreads();
-        if (tid == 0) {
-            int s = cur;
-            for (int sl = hi; sl >= lo; --sl) {
-                const int j = (s >> K) & (G::SP - 1);
-                const uint8_t* row = (const uint8_t*)stage + (size_t)(sl - lo) * G::BPSTEP;
-                s = j + bp_lookup<K>(row, j) * G::SP;
-                if (st) st[sl] = s;
-            }
-            cur = s;
-        }
+        if (tid == 0) cur = chase_links<K>((const uint8_t*)stage, hi, lo, st, cur);
         hi = lo - 1;
     }
     __syncthreads();
@@ -515,16 +566,7 @@ __device__ __forceinline__ void tb_chase_pf(const uint8_t* __restrict__ bpq, int
         __syncthreads();
         a0 = b0; a1 = b1; a2 = b2; a3 = b3;
         tb_chunk_load<K>(bpq, nsteps, stop, nc, c + 2, tid, b0, b1, b2, b3);
-        if (tid == 0) {
-            int s = cur;
-            for (int sl = hi; sl >= lo; --sl) {
-                const int j = (s >> K) & (G::SP - 1);
-                const uint8_t* row = (const uint8_t*)stage + (size_t)(sl - lo) * G::BPSTEP;
-                s = j + bp_lookup<K>(row, j) * G::SP;
-                if (st) st[sl] = s;
-            }
-            cur = s;
-        }
+        if (tid == 0) cur = chase_links<K>((const uint8_t*)stage, hi, lo, st, cur);
     }
     __syncthreads();
 }

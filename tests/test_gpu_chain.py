@@ -100,6 +100,23 @@ def test_chain_vs_oracle(xq, hb, oracle_mod, mul1_lut, K, k, n, pivot, margin):
     np.testing.assert_array_equal(hatW.numpy(), oracle_mod.decode(tr.numpy(), mul1_lut, K))
 
 
+@pytest.mark.parametrize("name,short,K", [("exl3_3inst", "3inst", 4), ("exl3_mcg", "mcg", 6)])
+def test_chain_other_codebooks(xq, hb, oracle_mod, name, short, K):
+    """The 3inst and mcg codebooks (fp16-exact, quantize.py:64-71) through the
+    chain: targets against the fp64 formula, states and packing against the
+    oracle with that codebook's table, decode with the same table."""
+    g = torch.Generator().manual_seed(60 + K)
+    W = torch.randn(96, 64, generator=g)
+    L = _lfac(xq, 96, K)
+    lut = oracle_mod.code_lut(name)
+    print(f"case chain code={short} K={K} 96x64", flush=True)
+    hatW, st, tr, xt = (t.cpu() for t in hb.ldlq_chain(W.cuda(), L.cuda(), K, 128, 0,
+                                                      code=short, targets=True))
+    _check_targets(W, L, hatW, xt, xq.tensor_core_perm())
+    _check_tiles(oracle_mod, lut, K, 128, 0, st, tr, xt)
+    np.testing.assert_array_equal(hatW.numpy(), oracle_mod.decode(tr.numpy(), lut, K))
+
+
 def test_chain_without_feedback(xq, hb, oracle_mod, mul1_lut):
     """L = None: every tile's targets are its own W values, and the encode is
     the plain tail-bite of each tile."""
