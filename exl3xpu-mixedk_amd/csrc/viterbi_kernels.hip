@@ -954,37 +954,46 @@ __global__ __launch_bounds__(kFwdThreads) void ldlq_chain_kernel(
             v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
             if (Lq != nullptr && i + 1 < tk) {
                 const int mstart = 16 * (i + 1), ngr = (k - mstart) >> 4;
-                const size_t q0 = (size_t)(mstart >> 2) * 64 + 64 * qq + 4 * rr;
-                const float* la = Lq + (size_t)i * 16 * k + q0;
-                const float* eb = Eq + (size_t)j * 16 * k + q0;
-                float4 pa[kChainDepth], pb[kChainDepth];
+                // wave-uniform operand bases (SGPRs) and 32-bit lane byte
+                // offsets; every load is issued (clamped to the last group,
+                // whose operands are then zeroed), so the waits count down
+                // through the kChainDepth groups in flight instead of
+                // draining them
+                const size_t qbase = (size_t)(mstart >> 2) * 64;
+                gbyte_t* const la = uniform_gptr((uint8_t*)(Lq + (size_t)i * 16 * k + qbase));
+                gbyte_t* const eb = uniform_gptr((uint8_t*)(Eq + (size_t)j * 16 * k + qbase));
+                const uint32_t lane = (uint32_t)(64 * qq + 4 * rr) * 4u;
+                auto goff = [&](int g) {
+                    return lane + (uint32_t)(g < ngr ? g : ngr - 1) * 1024u;
+                };
+                typedef __attribute__((address_space(1))) const v4f gv4_t;
+                v4f pa[kChainDepth], pb[kChainDepth];
 #pragma unroll
                 for (int d = 0; d < kChainDepth; ++d) {
-                    const int g = wv + 16 * d;
-                    pa[d] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                    pb[d] = pa[d];
-                    if (g < ngr) {
-                        pa[d] = *(const float4*)(la + 256 * g);
-                        pb[d] = *(const float4*)(eb + 256 * g);
-                    }
+                    const uint32_t o = goff(wv + 16 * d);
+                    pa[d] = *(gv4_t*)(la + o);
+                    pb[d] = *(gv4_t*)(eb + o);
                 }
+                // (the compiler barriers keep the prefetches where they are:
+                // otherwise the loads feeding the loop's phis are merged into
+                // one load at the top of the loop, right before their use)
+                asm volatile("" ::: "memory");
                 for (int g0 = wv; g0 < ngr; g0 += 16 * kChainDepth) {
 #pragma unroll
                     for (int d = 0; d < kChainDepth; ++d) {
                         const int g = g0 + 16 * d;
-                        if (g < ngr) {
-                            const float4 a = pa[d], b = pb[d];
-                            const int gn = g + 16 * kChainDepth;
-                            if (gn < ngr) {
-                                pa[d] = *(const float4*)(la + 256 * gn);
-                                pb[d] = *(const float4*)(eb + 256 * gn);
-                            }
-                            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, acc, 0, 0, 0);
-                            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, acc, 0, 0, 0);
-                            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, acc, 0, 0, 0);
-                            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, acc, 0, 0, 0);
-                        }
+                        const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
+                        const v4f a = (g < ngr) ? pa[d] : z, b = pb[d];
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, acc, 0, 0, 0);
+                        const uint32_t o = goff(g + 16 * kChainDepth);
+                        pa[d] = *(gv4_t*)(la + o);
+                        pb[d] = *(gv4_t*)(eb + o);
+                        __builtin_amdgcn_sched_barrier(0);   // issued right after their use
                     }
+                    asm volatile("" ::: "memory");
                 }
             }
 #pragma unroll
