@@ -44,6 +44,13 @@ hipError_t launch_forward(int K, const float* X, int xstride, int xlen, int nseq
                           const int32_t* ov_in, void* bp, int32_t* send, uint32_t* err,
                           int group, hipStream_t stream);
 
+// launch_forward for K=3 (same arguments); defined in the K=3 translation
+// unit (viterbi_kernels.hip built with XTQ_FWD_K3_TU).
+hipError_t launch_forward_k3(const float* X, int xstride, int xlen, int nseq,
+                             const uint16_t* lut16, int roll, int nsteps, int store_lo,
+                             const int32_t* ov_in, void* bp, int32_t* send, uint32_t* err,
+                             int group, hipStream_t stream);
+
 // Both tail-biting passes of nseq sequences (256-step targets X [nseq][256])
 // in one launch of 2*nseq workgroups (see tailbite_fused_kernel): pass 1
 // free on X rolled by pivot for n1 steps, traced back in-kernel to

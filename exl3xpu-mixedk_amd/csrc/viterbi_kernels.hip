@@ -26,6 +26,11 @@
 //     lexicographic order (cost, index) -- the reference's tie rule;
 //   * backpointers are K bits per group, packed per thread and written
 //     coalesced to HBM; a separate traceback kernel stages them through LDS.
+//
+// Built twice: as the library's kernels, and with XTQ_FWD_K3_TU defined as
+// the translation unit of K=3's batched forward alone (launch_forward_k3),
+// which is compiled under the max-ilp scheduling strategy (faster for that
+// kernel only; every other kernel measured slower under it).
 #include "viterbi_kernels.h"
 
 #pragma clang fp contract(off)
@@ -1119,6 +1124,19 @@ struct FwdL {
     }
 };
 
+#ifndef XTQ_FWD_K3_TU
+template <>
+struct FwdL<3> {
+    static hipError_t run(const float* X, int xstride, int xlen, int nseq,
+                          const uint16_t* lut16, int roll, int nsteps, int store_lo,
+                          const int32_t* ov_in, void* bp, int32_t* send, uint32_t* err,
+                          int group, hipStream_t s) {
+        return launch_forward_k3(X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo, ov_in,
+                                 bp, send, err, group, s);
+    }
+};
+#endif
+
 template <int K>
 struct GroupSel {
     static hipError_t run(int nseq, int ncu, int* out) {
@@ -1214,6 +1232,15 @@ struct StepBytes {
 
 }  // namespace
 
+#ifdef XTQ_FWD_K3_TU
+hipError_t launch_forward_k3(const float* X, int xstride, int xlen, int nseq,
+                             const uint16_t* lut16, int roll, int nsteps, int store_lo,
+                             const int32_t* ov_in, void* bp, int32_t* send, uint32_t* err,
+                             int group, hipStream_t stream) {
+    return FwdL<3>::run(X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo, ov_in, bp, send,
+                        err, group, stream);
+}
+#else
 size_t bp_step_bytes(int K) {
     size_t b = 0;
     if (dispatch_k<StepBytes>(K, &b) != hipSuccess) return 0;
@@ -1299,5 +1326,7 @@ hipError_t launch_unpack(int K, const int16_t* trellis, int nt, int32_t* states,
     if (nt <= 0) return hipSuccess;
     return dispatch_k<UnpackL>(K, trellis, nt, states, stream);
 }
+
+#endif  // XTQ_FWD_K3_TU
 
 }  // namespace xtq
