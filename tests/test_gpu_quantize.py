@@ -182,3 +182,29 @@ def test_gaussian_mse(xq, K):
     dec = lut[st]
     mse = (dec - X).square().mean() / X.square().mean()
     assert mse < 3.0 * 2.0 ** (-2 * K)
+
+
+def test_block_ldl_device_large(xq):
+    """block_LDL of a device matrix at the size that takes the MAGMA Cholesky
+    (when the build has it): L D L^T reproduces G to fp32 accuracy against
+    the fp64 factor, the diagonal blocks are identities, torch's preferred
+    linalg backend is restored afterwards, and a matrix that is not positive
+    definite raises RuntimeError (the damping fallback relies on it)."""
+    import workloads as wl
+    n = xq._MAGMA_CHOL_MIN
+    G = wl.ar1_gram(n, 2048, 0.5, 11, device="cuda").float()
+    G.diagonal().add_(0.01 * G.diagonal().mean())
+    before = torch.backends.cuda.preferred_linalg_library()
+    L, D = xq.block_LDL(G.clone(), 16)
+    assert torch.backends.cuda.preferred_linalg_library() == before
+    L64, D64 = xq.block_LDL(G.double(), 16)
+    assert float((L.double() - L64).norm() / L64.norm()) < 1e-4
+    R = L.double() @ torch.block_diag(*D.double()) @ L.double().t()
+    assert float((R - G.double()).norm() / G.double().norm()) < 1e-5
+    m = n // 16
+    diag = torch.diagonal(L.view(m, 16, m, 16), dim1=0, dim2=2).permute(2, 0, 1)
+    assert torch.equal(diag, torch.eye(16, device="cuda").expand(m, 16, 16))
+    B = torch.randn(n, n, device="cuda")
+    with pytest.raises(RuntimeError):
+        xq.block_LDL(B + B.t(), 16)
+    assert torch.backends.cuda.preferred_linalg_library() == before
