@@ -164,9 +164,11 @@ __device__ __forceinline__ int bp_lookup(const uint8_t* row, int j) {
 }
 
 // --------------------------------------------------------------- forward DP
-// Whether the candidate arithmetic is issued grouped by opcode (see fwd_run).
-template <int K>
-constexpr bool kGroupOps = (K >= 5);
+// Whether the candidate arithmetic is issued grouped by opcode (see fwd_run):
+// measured faster for K >= 6, and for K = 5 with T >= 2 sequences per
+// workgroup; at T = 1 (the column chain) K = 5 is 3 % faster ungrouped.
+template <int K, int T>
+constexpr bool kGroupOps = (K >= 6) || (K == 5 && T >= 2);
 
 // Shared memory of one forward run over T sequences.
 template <int K, int T>
@@ -279,7 +281,7 @@ __device__ __forceinline__ void fwd_run(
                 for (int c = 0; c < G::C; ++c) {
                     const int blk = c / G::CB;
                     double kk[G::NCH];
-                    if constexpr (kGroupOps<K>) {
+                    if constexpr (kGroupOps<K, T>) {
                         // Issue the chunk's candidates opcode by opcode (all
                         // subs, then all squares, then all adds): gfx950
                         // issues adjacent independent v_mul_f32 / v_add_f32
@@ -304,8 +306,8 @@ __device__ __forceinline__ void fwd_run(
                         for (int w = 0; w < G::NCH; ++w)
                             kk[w] = key_of(tag[w], dv[w] + B[blk][w]);
                     } else {
-                        // K <= 4: the compiler's own interleaving measures
-                        // faster.
+                        // K <= 4, and K = 5 at T = 1: the compiler's own
+                        // interleaving measures faster.
 #pragma unroll
                         for (int w = 0; w < G::NCH; ++w) {
                             const int l = c * G::W + qc * G::NCH + w;
