@@ -1,13 +1,15 @@
 // valu_probe.hip -- VALU issue-rate measurement for the forward DP's roofline.
 //
-// The forward DP spends one v_fma_mix_f32 (sub), v_mul_f32 (square),
-// v_add_f32 (add) and v_min_f64 (min/argmin) per trellis candidate.  On
-// gfx950 those instructions do not all issue at one wave64 instruction per
-// SIMD per 4 cycles: independent v_mul_f32 / v_add_f32 placed next to each
-// other issue faster.  These kernels time each instruction alone and the
-// four-instruction candidate mix (in dependency order and grouped by opcode)
-// on every CU, so the benchmark can report the kernel against the ceiling
-// its own instruction mix has on the GPU it runs on.
+// The forward DP spends four instructions per trellis candidate: the
+// subtraction (v_add_f32 of -x with the codebook held in fp32 registers, or
+// v_fma_mix_f32 with it held as packed fp16 pairs), v_mul_f32 (square),
+// v_add_f32 (add) and v_min_f64 (min/argmin).  On gfx950 those instructions
+// do not all issue at one wave64 instruction per SIMD per 4 cycles:
+// independent v_mul_f32 / v_add_f32 placed next to each other issue faster.
+// These kernels time each instruction alone and both four-instruction
+// candidate mixes (in dependency order and grouped by opcode) on every CU, so
+// the benchmark can report the kernel against the ceiling its own
+// instruction mix has on the GPU it runs on.
 //
 // Each thread runs kChains independent chains for kIters iterations and
 // writes one float; nothing else is read or written.
@@ -54,6 +56,29 @@ __global__ __launch_bounds__(kThreads) void probe_kernel(float* __restrict__ out
 #pragma unroll
             for (int c = 0; c < kChains; ++c)
                 asm volatile("v_min_f64 %0, %0, %1" : "+v"(d[c]) : "v"((double)b));
+        } else if constexpr (OP == 7) {               // fp32-code mix, dependency order
+#pragma unroll
+            for (int c = 0; c < kChains; ++c) {
+                asm volatile("v_add_f32 %0, %1, %2" : "=v"(x[c]) : "v"(x[c]), "v"(b));
+                asm volatile("v_mul_f32 %0, %0, %0" : "+v"(x[c]));
+                asm volatile("v_add_f32 %0, %0, %1" : "+v"(x[c]) : "v"(b));
+                asm volatile("v_min_f64 %0, %0, %1" : "+v"(d[c]) : "v"((double)b));
+            }
+        } else if constexpr (OP == 8) {               // fp32-code mix, grouped by 8
+#pragma unroll
+            for (int g0 = 0; g0 < kChains; g0 += 8) {
+#pragma unroll
+                for (int c = g0; c < g0 + 8; ++c)
+                    asm volatile("v_add_f32 %0, %1, %2" : "=v"(x[c]) : "v"(x[c]), "v"(b));
+#pragma unroll
+                for (int c = g0; c < g0 + 8; ++c) asm volatile("v_mul_f32 %0, %0, %0" : "+v"(x[c]));
+#pragma unroll
+                for (int c = g0; c < g0 + 8; ++c)
+                    asm volatile("v_add_f32 %0, %0, %1" : "+v"(x[c]) : "v"(b));
+#pragma unroll
+                for (int c = g0; c < g0 + 8; ++c)
+                    asm volatile("v_min_f64 %0, %0, %1" : "+v"(d[c]) : "v"((double)b));
+            }
         } else if constexpr (OP == 5) {               // candidate mix, dependency order
 #pragma unroll
             for (int c = 0; c < kChains; ++c) {
@@ -88,7 +113,7 @@ __global__ __launch_bounds__(kThreads) void probe_kernel(float* __restrict__ out
 }
 
 // VALU instructions per chain per iteration of each probe.
-constexpr int kOpsPerChain[7] = {1, 1, 1, 1, 1, 4, 4};
+constexpr int kOpsPerChain[9] = {1, 1, 1, 1, 1, 4, 4, 4, 4};
 
 template <int OP>
 hipError_t launch(int nwg, float* out, hipStream_t s) {
@@ -104,7 +129,9 @@ hipError_t launch_any(int which, int nwg, float* out, hipStream_t s) {
         case 3: return launch<3>(nwg, out, s);
         case 4: return launch<4>(nwg, out, s);
         case 5: return launch<5>(nwg, out, s);
-        default: return launch<6>(nwg, out, s);
+        case 6: return launch<6>(nwg, out, s);
+        case 7: return launch<7>(nwg, out, s);
+        default: return launch<8>(nwg, out, s);
     }
 }
 
@@ -112,7 +139,7 @@ hipError_t launch_any(int which, int nwg, float* out, hipStream_t s) {
 
 extern "C" int xtq_valu_probe(int which, double* lane_ops_per_s) {
     if (!lane_ops_per_s) return 12;
-    if (which < 0 || which > 6) return 8;
+    if (which < 0 || which > 8) return 8;
     int dev = 0, ncu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||

@@ -14,9 +14,11 @@
 //   * thread t owns the C = SP/1024 consecutive groups j = t*C .. t*C+C-1
 //     (K=7: half of group t/2) and the candidate states of each,
 //     s = j + w*SP, i.e. 64 states per thread for every K; their codebook
-//     values stay in 32 VGPRs as packed fp16 pairs for the whole kernel
-//     (every supported codebook is fp16-exact), are shared by the T
-//     sequences and are widened exactly inside v_fma_mix_f32;
+//     values (every supported codebook is fp16-exact) stay in registers for
+//     the whole kernel, shared by the T sequences: as 64 fp32 VGPRs, so
+//     that fl(f - x) is a v_add_f32 of -x on the fast issue path, or, where
+//     that would spill, as 32 VGPRs of packed fp16 pairs widened exactly
+//     inside v_fma_mix_f32 (kF32Code);
 //   * the per-group minima b (SP floats per sequence) are the only state
 //     carried between steps; they live in LDS, double buffered, one barrier
 //     per step for all T sequences;
@@ -170,6 +172,14 @@ __device__ __forceinline__ int bp_lookup(const uint8_t* row, int j) {
 template <int K, int T>
 constexpr bool kGroupOps = (K >= 6) || (K == 5 && T >= 2);
 
+// Whether the codebook values are held as fp32 (64 VGPRs: fl(f - x) is a
+// v_add_f32, which gfx950 issues on its fast path, where v_fma_mix_f32 takes
+// the full 4 cycles) or as packed fp16 pairs (32 VGPRs).  fp32 measured
+// 4-22 % faster wherever the kernel still fits 128 VGPRs; K=5 at T >= 2 and
+// K=7 at T = 1 (the column chain) spill with it and keep the fp16 pairs.
+template <int K, int T>
+constexpr bool kF32Code = !((K == 5 && T >= 2) || (K == 7 && T == 1));
+
 // Shared memory of one forward run over T sequences.
 template <int K, int T>
 struct FwdSmem {
@@ -214,17 +224,35 @@ __device__ __forceinline__ void fwd_run(
     // group is state j_c + (wbase + w) * SP; local index l = c*W + w.
     const int jbase = G::HALF ? (tid >> 1) : tid * G::C;
     const int wbase = G::HALF ? (tid & 1) * G::W : 0;
-    h2_t fh[G::NSTATE / 2];
+    constexpr bool F32 = kF32Code<K, T>;
+    h2_t fh[F32 ? 1 : G::NSTATE / 2];
+    float f32[F32 ? G::NSTATE : 1];
+    if constexpr (F32) {
 #pragma unroll
-    for (int l = 0; l < G::NSTATE / 2; ++l) {
-        const int l0 = 2 * l, l1 = 2 * l + 1;
-        const int s0 = jbase + l0 / G::W + (wbase + l0 % G::W) * G::SP;
-        const int s1 = jbase + l1 / G::W + (wbase + l1 % G::W) * G::SP;
-        h2_t v;
-        v.x = __builtin_bit_cast(_Float16, lut16[s0]);
-        v.y = __builtin_bit_cast(_Float16, lut16[s1]);
-        fh[l] = v;
+        for (int l = 0; l < G::NSTATE; ++l)
+            f32[l] = (float)__builtin_bit_cast(
+                _Float16, lut16[jbase + l / G::W + (wbase + l % G::W) * G::SP]);
+    } else {
+#pragma unroll
+        for (int l = 0; l < G::NSTATE / 2; ++l) {
+            const int l0 = 2 * l, l1 = 2 * l + 1;
+            const int s0 = jbase + l0 / G::W + (wbase + l0 % G::W) * G::SP;
+            const int s1 = jbase + l1 / G::W + (wbase + l1 % G::W) * G::SP;
+            h2_t v;
+            v.x = __builtin_bit_cast(_Float16, lut16[s0]);
+            v.y = __builtin_bit_cast(_Float16, lut16[s1]);
+            fh[l] = v;
+        }
     }
+    // fl(f_l - x) for the state of local index l (a single rounding either
+    // way: f is exact in fp32, and the fma with 1.0 rounds once)
+    auto fsub = [&](int l, float negx) {
+        if constexpr (F32)
+            return f32[l] + negx;
+        else
+            return __builtin_fmaf((l & 1) ? (float)fh[l >> 1].y : (float)fh[l >> 1].x, one,
+                                  negx);
+    };
     // Per-lane key tags: distinct per lane so they stay in VGPRs next to the
     // cost they are paired with; the low byte is the candidate index.
     uint32_t tag[G::NCH];
@@ -253,11 +281,17 @@ __device__ __forceinline__ void fwd_run(
         const int u = (i - roll < 0) ? i - roll + xlen : i - roll;
 #pragma unroll 1
         for (int tt = 0; tt < ntile; ++tt) {
-            // Keep the fp16 codebook pairs opaque per sequence-step so the
-            // widening stays inside v_fma_mix_f32 instead of being hoisted
-            // into fp32 VGPRs.
+            // Keep the codebook registers opaque per sequence-step: the fp16
+            // pairs so that the widening stays inside v_fma_mix_f32 instead
+            // of being hoisted into fp32 VGPRs, the fp32 values so that they
+            // stay put rather than being re-derived.
+            if constexpr (F32) {
 #pragma unroll
-            for (int l = 0; l < G::NSTATE / 2; ++l) asm volatile("" : "+v"(fh[l]));
+                for (int l = 0; l < G::NSTATE; ++l) asm volatile("" : "+v"(f32[l]));
+            } else {
+#pragma unroll
+                for (int l = 0; l < G::NSTATE / 2; ++l) asm volatile("" : "+v"(fh[l]));
+            }
             const int q = q0 + tt;
             const float negx = -__int_as_float(
                 __builtin_amdgcn_readfirstlane(__float_as_int(xs[tt][u])));
@@ -291,10 +325,7 @@ __device__ __forceinline__ void fwd_run(
                         float dv[G::NCH];
 #pragma unroll
                         for (int w = 0; w < G::NCH; ++w) {
-                            const int l = c * G::W + qc * G::NCH + w;
-                            const float fv =
-                                (l & 1) ? (float)fh[l >> 1].y : (float)fh[l >> 1].x;
-                            dv[w] = __builtin_fmaf(fv, one, negx);  // == fl(f - x)
+                            dv[w] = fsub(c * G::W + qc * G::NCH + w, negx);
                         }
 #pragma unroll
                         for (int w = 0; w < G::NCH; ++w) asm volatile("" : "+v"(dv[w]));
@@ -310,10 +341,7 @@ __device__ __forceinline__ void fwd_run(
                         // interleaving measures faster.
 #pragma unroll
                         for (int w = 0; w < G::NCH; ++w) {
-                            const int l = c * G::W + qc * G::NCH + w;
-                            const float fv =
-                                (l & 1) ? (float)fh[l >> 1].y : (float)fh[l >> 1].x;
-                            const float d = __builtin_fmaf(fv, one, negx);  // == fl(f - x)
+                            const float d = fsub(c * G::W + qc * G::NCH + w, negx);
                             const float e = d * d;
                             kk[w] = key_of(tag[w], e + B[blk][w]);
                         }

@@ -290,7 +290,9 @@ def prof_enable(on: bool = True):
 
 
 VALU_PROBES = ("v_mul_f32", "v_add_f32", "v_fma_f32", "v_fma_mix_f32", "v_min_f64",
-               "candidate mix, dependency order", "candidate mix, grouped by opcode")
+               "candidate mix, dependency order", "candidate mix, grouped by opcode",
+               "fp32-code candidate mix, dependency order",
+               "fp32-code candidate mix, grouped by opcode")
 
 
 def valu_probe(which: int) -> float:

@@ -224,8 +224,11 @@ XTQ_API int xtq_vit_prof_read(double* fwd_ms, int64_t* fwd_launches, double* fwd
  * the forward DP's roofline).  Times one probe kernel on every CU of the
  * current device and returns its VALU lane-instructions per second:
  *   0 v_mul_f32, 1 v_add_f32, 2 v_fma_f32, 3 v_fma_mix_f32, 4 v_min_f64,
- *   5 the DP's candidate mix (v_fma_mix_f32, v_mul_f32, v_add_f32,
- *     v_min_f64) in dependency order, 6 the same mix grouped by opcode.
+ *   5 the DP's candidate mix with the codebook as packed fp16 (v_fma_mix_f32,
+ *     v_mul_f32, v_add_f32, v_min_f64) in dependency order, 6 the same mix
+ *     grouped by opcode, 7 the mix with the codebook in fp32 (v_add_f32,
+ *     v_mul_f32, v_add_f32, v_min_f64) in dependency order, 8 that mix
+ *     grouped by opcode.
  * Returns 8 for an unknown probe, 2 if its small output buffer cannot be
  * allocated, 4 on a HIP error.
  */

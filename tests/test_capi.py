@@ -95,7 +95,8 @@ def test_status_codes_without_device(lib):
     assert chm(fake, None, 64, 64, 2, i2(32, 32), i2(4, 7), *args, tp1, None, None) == 12
     assert chm(fake, None, 64, 64, 2, None, i2(4, 7), *args, tp2, None, None) == 12
     out = ctypes.c_double()
-    assert lib.xtq_valu_probe(7, ctypes.byref(out)) == 8
+    assert lib.xtq_valu_probe(9, ctypes.byref(out)) == 8
+    assert lib.xtq_valu_probe(-1, ctypes.byref(out)) == 8
     assert lib.xtq_valu_probe(0, None) == 12
     assert lib.xtq_vit_strerror(11) == b"NaN target"
     assert lib.xtq_vit_strerror(99) == b"unknown status"
