@@ -175,10 +175,16 @@ constexpr bool kGroupOps = (K >= 6) || (K == 5 && T >= 2);
 // Whether the codebook values are held as fp32 (64 VGPRs: fl(f - x) is a
 // v_add_f32, which gfx950 issues on its fast path, where v_fma_mix_f32 takes
 // the full 4 cycles) or as packed fp16 pairs (32 VGPRs).  fp32 measured
-// 4-22 % faster wherever the kernel still fits 128 VGPRs; K=5 at T >= 2 and
-// K=7 at T = 1 (the column chain) spill with it and keep the fp16 pairs.
+// 4-22 % faster wherever the kernel still fits 128 VGPRs; K=5 at T >= 2
+// spills with it and keeps the fp16 pairs.
 template <int K, int T>
-constexpr bool kF32Code = !((K == 5 && T >= 2) || (K == 7 && T == 1));
+constexpr bool kF32Code = !(K == 5 && T >= 2);
+
+// Candidates per chunk of the min tree: 16, or 8 for K=7 at T = 1, where the
+// smaller chunk's keys leave the column-chain kernel room for the fp32
+// codebook (its K=7 sweep: 0.42 -> 0.36 s).
+template <int K, int T>
+constexpr int kChunkW = (K == 7 && T == 1) ? 8 : Geom<K>::NCH;
 
 // Shared memory of one forward run over T sequences.
 template <int K, int T>
@@ -225,6 +231,8 @@ __device__ __forceinline__ void fwd_run(
     const int jbase = G::HALF ? (tid >> 1) : tid * G::C;
     const int wbase = G::HALF ? (tid & 1) * G::W : 0;
     constexpr bool F32 = kF32Code<K, T>;
+    constexpr int NCH = kChunkW<K, T>;          // candidates per chunk
+    constexpr int NCHUNK = G::W / NCH;
     h2_t fh[F32 ? 1 : G::NSTATE / 2];
     float f32[F32 ? G::NSTATE : 1];
     if constexpr (F32) {
@@ -255,9 +263,9 @@ __device__ __forceinline__ void fwd_run(
     };
     // Per-lane key tags: distinct per lane so they stay in VGPRs next to the
     // cost they are paired with; the low byte is the candidate index.
-    uint32_t tag[G::NCH];
+    uint32_t tag[NCH];
 #pragma unroll
-    for (int w = 0; w < G::NCH; ++w) tag[w] = ((uint32_t)tid << 8) | (uint32_t)(wbase + w);
+    for (int w = 0; w < NCH; ++w) tag[w] = ((uint32_t)tid << 8) | (uint32_t)(wbase + w);
     __syncthreads();
 
     // Start mask b_0: 0 everywhere (free) or 0 only at group ov (pinned).
@@ -299,11 +307,11 @@ __device__ __forceinline__ void fwd_run(
 
             double run[G::C];
 #pragma unroll
-            for (int qc = 0; qc < G::NCHUNK; ++qc) {
-                float B[G::NB][G::NCH];
+            for (int qc = 0; qc < NCHUNK; ++qc) {
+                float B[G::NB][NCH];
 #pragma unroll
-                for (int w = 0; w < G::NCH; ++w) {
-                    const float* src = bcur + a0 + rpad + (wbase + qc * G::NCH + w) * G::Q;
+                for (int w = 0; w < NCH; ++w) {
+                    const float* src = bcur + a0 + rpad + (wbase + qc * NCH + w) * G::Q;
                     if constexpr (G::NB == 4) {
                         const float4 v = *(const float4*)src;
                         B[0][w] = v.x; B[1][w] = v.y; B[2][w] = v.z; B[3][w] = v.w;
@@ -314,7 +322,7 @@ __device__ __forceinline__ void fwd_run(
 #pragma unroll
                 for (int c = 0; c < G::C; ++c) {
                     const int blk = c / G::CB;
-                    double kk[G::NCH];
+                    double kk[NCH];
                     if constexpr (kGroupOps<K, T>) {
                         // Issue the chunk's candidates opcode by opcode (all
                         // subs, then all squares, then all adds): gfx950
@@ -322,38 +330,38 @@ __device__ __forceinline__ void fwd_run(
                         // faster than one per 4 cycles, which a
                         // dependency-ordered schedule forfeits; the empty asm
                         // statements fix the phase order.
-                        float dv[G::NCH];
+                        float dv[NCH];
 #pragma unroll
-                        for (int w = 0; w < G::NCH; ++w) {
-                            dv[w] = fsub(c * G::W + qc * G::NCH + w, negx);
+                        for (int w = 0; w < NCH; ++w) {
+                            dv[w] = fsub(c * G::W + qc * NCH + w, negx);
                         }
 #pragma unroll
-                        for (int w = 0; w < G::NCH; ++w) asm volatile("" : "+v"(dv[w]));
+                        for (int w = 0; w < NCH; ++w) asm volatile("" : "+v"(dv[w]));
 #pragma unroll
-                        for (int w = 0; w < G::NCH; ++w) dv[w] = dv[w] * dv[w];
+                        for (int w = 0; w < NCH; ++w) dv[w] = dv[w] * dv[w];
 #pragma unroll
-                        for (int w = 0; w < G::NCH; ++w) asm volatile("" : "+v"(dv[w]));
+                        for (int w = 0; w < NCH; ++w) asm volatile("" : "+v"(dv[w]));
 #pragma unroll
-                        for (int w = 0; w < G::NCH; ++w)
+                        for (int w = 0; w < NCH; ++w)
                             kk[w] = key_of(tag[w], dv[w] + B[blk][w]);
                     } else {
                         // K <= 4, and K = 5 at T = 1: the compiler's own
                         // interleaving measures faster.
 #pragma unroll
-                        for (int w = 0; w < G::NCH; ++w) {
-                            const float d = fsub(c * G::W + qc * G::NCH + w, negx);
+                        for (int w = 0; w < NCH; ++w) {
+                            const float d = fsub(c * G::W + qc * NCH + w, negx);
                             const float e = d * d;
                             kk[w] = key_of(tag[w], e + B[blk][w]);
                         }
                     }
 #pragma unroll
-                    for (int st = 1; st < G::NCH; st *= 2)
+                    for (int st = 1; st < NCH; st *= 2)
 #pragma unroll
-                        for (int w = 0; w < G::NCH; w += 2 * st) kk[w] = kmin(kk[w], kk[w + st]);
+                        for (int w = 0; w < NCH; w += 2 * st) kk[w] = kmin(kk[w], kk[w + st]);
                     if (qc == 0) {
                         run[c] = kk[0];
                     } else {
-                        const double kq = key_of(key_lo(kk[0]) + (uint32_t)(qc * G::NCH),
+                        const double kq = key_of(key_lo(kk[0]) + (uint32_t)(qc * NCH),
                                                  key_cost(kk[0]));
                         run[c] = kmin(run[c], kq);
                     }
