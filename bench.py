@@ -437,9 +437,9 @@ def main():
                 "traceback_ms_per_step": round(prof["tb_ms"] / args.steps, 3),
                 "whole_job_frac": round(tps * OPS_PER_STATE_STEP * 65536 * 512 / VALU_PEAK, 4)}
     probes = {name: hb.valu_probe(i) / 1e12 for i, name in enumerate(hb.VALU_PROBES)}
-    # the ceiling of the instruction mix the timed kernel issues: its codebook
-    # is held in fp32 (subtraction by v_add_f32) at every K but 5
-    mix = "fp32-code candidate mix" if args.k != 5 else "candidate mix"
+    # the ceiling of the instruction mix the timed kernel issues (codebook in
+    # fp32 registers: the subtraction is a v_add_f32)
+    mix = "fp32-code candidate mix"
     ceil = max(probes[f"{mix}, dependency order"], probes[f"{mix}, grouped by opcode"])
     roofline["mix_ceiling"] = {"value": round(ceil, 3), "unit": "TOP/s", "mix": mix,
                                "frac": round(achieved / ceil, 4),

@@ -14,11 +14,11 @@
 //   * thread t owns the C = SP/1024 consecutive groups j = t*C .. t*C+C-1
 //     (K=7: half of group t/2) and the candidate states of each,
 //     s = j + w*SP, i.e. 64 states per thread for every K; their codebook
-//     values (every supported codebook is fp16-exact) stay in registers for
-//     the whole kernel, shared by the T sequences: as 64 fp32 VGPRs, so
-//     that fl(f - x) is a v_add_f32 of -x on the fast issue path, or, where
-//     that would spill, as 32 VGPRs of packed fp16 pairs widened exactly
-//     inside v_fma_mix_f32 (kF32Code);
+//     values (every supported codebook is fp16-exact, hence exact in fp32)
+//     stay in 64 fp32 VGPRs for the whole kernel, shared by the T
+//     sequences, so that fl(f - x) is one v_add_f32 of -x, an instruction
+//     gfx950 issues on its fast path (the packed fp16 pairs plus
+//     v_fma_mix_f32 of earlier versions took 32 VGPRs but a full 4 cycles);
 //   * the per-group minima b (SP floats per sequence) are the only state
 //     carried between steps; they live in LDS, double buffered, one barrier
 //     per step for all T sequences;
@@ -40,7 +40,6 @@
 namespace xtq {
 namespace {
 
-typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 
 template <int K>
 struct Geom {
@@ -172,19 +171,12 @@ __device__ __forceinline__ int bp_lookup(const uint8_t* row, int j) {
 template <int K, int T>
 constexpr bool kGroupOps = (K >= 6) || (K == 5 && T >= 2);
 
-// Whether the codebook values are held as fp32 (64 VGPRs: fl(f - x) is a
-// v_add_f32, which gfx950 issues on its fast path, where v_fma_mix_f32 takes
-// the full 4 cycles) or as packed fp16 pairs (32 VGPRs).  fp32 measured
-// 4-22 % faster wherever the kernel still fits 128 VGPRs; K=5 at T >= 2
-// spills with it and keeps the fp16 pairs.
+// Candidates per chunk of the min tree: 16, or 8 for K=5 at T >= 2 and for
+// K=7 at T = 1, where the smaller chunk's keys make room for the fp32
+// codebook registers (16-wide chunks spilled there: K=5 batched 285k ->
+// 367k tiles/s, the K=7 column chain 0.42 -> 0.36 s with 8).
 template <int K, int T>
-constexpr bool kF32Code = !(K == 5 && T >= 2);
-
-// Candidates per chunk of the min tree: 16, or 8 for K=7 at T = 1, where the
-// smaller chunk's keys leave the column-chain kernel room for the fp32
-// codebook (its K=7 sweep: 0.42 -> 0.36 s).
-template <int K, int T>
-constexpr int kChunkW = (K == 7 && T == 1) ? 8 : Geom<K>::NCH;
+constexpr int kChunkW = ((K == 5 && T >= 2) || (K == 7 && T == 1)) ? 8 : Geom<K>::NCH;
 
 // Shared memory of one forward run over T sequences.
 template <int K, int T>
@@ -206,7 +198,7 @@ template <int K, int T>
 __device__ __forceinline__ void fwd_run(
     FwdSmem<K, T>& sm, const float* __restrict__ X, int xstride, int xlen, int q0, int ntile,
     const uint16_t* __restrict__ lut16, int roll, int nsteps, int store_lo, bool pinned,
-    uint8_t* __restrict__ bp, int32_t* send, uint32_t* __restrict__ err, float one, int tid) {
+    uint8_t* __restrict__ bp, int32_t* send, uint32_t* __restrict__ err, int tid) {
     using G = Geom<K>;
     auto& bbuf = sm.bbuf;
     auto& xs = sm.xs;
@@ -230,37 +222,17 @@ __device__ __forceinline__ void fwd_run(
     // group is state j_c + (wbase + w) * SP; local index l = c*W + w.
     const int jbase = G::HALF ? (tid >> 1) : tid * G::C;
     const int wbase = G::HALF ? (tid & 1) * G::W : 0;
-    constexpr bool F32 = kF32Code<K, T>;
     constexpr int NCH = kChunkW<K, T>;          // candidates per chunk
     constexpr int NCHUNK = G::W / NCH;
-    h2_t fh[F32 ? 1 : G::NSTATE / 2];
-    float f32[F32 ? G::NSTATE : 1];
-    if constexpr (F32) {
+    // codebook value of local state l, exact in fp32
+    float f32[G::NSTATE];
 #pragma unroll
-        for (int l = 0; l < G::NSTATE; ++l)
-            f32[l] = (float)__builtin_bit_cast(
-                _Float16, lut16[jbase + l / G::W + (wbase + l % G::W) * G::SP]);
-    } else {
-#pragma unroll
-        for (int l = 0; l < G::NSTATE / 2; ++l) {
-            const int l0 = 2 * l, l1 = 2 * l + 1;
-            const int s0 = jbase + l0 / G::W + (wbase + l0 % G::W) * G::SP;
-            const int s1 = jbase + l1 / G::W + (wbase + l1 % G::W) * G::SP;
-            h2_t v;
-            v.x = __builtin_bit_cast(_Float16, lut16[s0]);
-            v.y = __builtin_bit_cast(_Float16, lut16[s1]);
-            fh[l] = v;
-        }
-    }
-    // fl(f_l - x) for the state of local index l (a single rounding either
-    // way: f is exact in fp32, and the fma with 1.0 rounds once)
-    auto fsub = [&](int l, float negx) {
-        if constexpr (F32)
-            return f32[l] + negx;
-        else
-            return __builtin_fmaf((l & 1) ? (float)fh[l >> 1].y : (float)fh[l >> 1].x, one,
-                                  negx);
-    };
+    for (int l = 0; l < G::NSTATE; ++l)
+        f32[l] = (float)__builtin_bit_cast(
+            _Float16, lut16[jbase + l / G::W + (wbase + l % G::W) * G::SP]);
+    // fl(f_l - x): one rounding of the exact difference, as the reference's
+    // fp32 subtraction
+    auto fsub = [&](int l, float negx) { return f32[l] + negx; };
     // Per-lane key tags: distinct per lane so they stay in VGPRs next to the
     // cost they are paired with; the low byte is the candidate index.
     uint32_t tag[NCH];
@@ -289,17 +261,10 @@ __device__ __forceinline__ void fwd_run(
         const int u = (i - roll < 0) ? i - roll + xlen : i - roll;
 #pragma unroll 1
         for (int tt = 0; tt < ntile; ++tt) {
-            // Keep the codebook registers opaque per sequence-step: the fp16
-            // pairs so that the widening stays inside v_fma_mix_f32 instead
-            // of being hoisted into fp32 VGPRs, the fp32 values so that they
-            // stay put rather than being re-derived.
-            if constexpr (F32) {
+            // Keep the codebook registers opaque per sequence-step so that
+            // they stay put in VGPRs rather than being re-derived.
 #pragma unroll
-                for (int l = 0; l < G::NSTATE; ++l) asm volatile("" : "+v"(f32[l]));
-            } else {
-#pragma unroll
-                for (int l = 0; l < G::NSTATE / 2; ++l) asm volatile("" : "+v"(fh[l]));
-            }
+            for (int l = 0; l < G::NSTATE; ++l) asm volatile("" : "+v"(f32[l]));
             const int q = q0 + tt;
             const float negx = -__int_as_float(
                 __builtin_amdgcn_readfirstlane(__float_as_int(xs[tt][u])));
@@ -462,8 +427,7 @@ __global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
     const float* __restrict__ X, int xstride, int xlen, int nseq,
     const uint16_t* __restrict__ lut16, int roll, int nsteps, int store_lo,
     const int32_t* __restrict__ ov_in,
-    uint8_t* __restrict__ bp, int32_t* __restrict__ send, uint32_t* __restrict__ err,
-    float one) {
+    uint8_t* __restrict__ bp, int32_t* __restrict__ send, uint32_t* __restrict__ err) {
     __shared__ FwdSmem<K, T> sm;
     const int q0 = blockIdx.x * T;
     const int ntile = (nseq - q0) < T ? (nseq - q0) : T;   // sequences in this group
@@ -471,7 +435,7 @@ __global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
     if (threadIdx.x < T)
         sm.ovs[threadIdx.x] = (pinned && (int)threadIdx.x < ntile) ? ov_in[q0 + threadIdx.x] : -1;
     fwd_run<K, T>(sm, X, xstride, xlen, q0, ntile, lut16, roll, nsteps, store_lo, pinned, bp,
-                  send + q0, err, one, (int)threadIdx.x);
+                  send + q0, err, (int)threadIdx.x);
 }
 
 // ---------------------------------------------------------------- traceback
@@ -730,7 +694,7 @@ __global__ __launch_bounds__(kFwdThreads) void tailbite_fused_kernel(
     const float* __restrict__ X, int nseq, const uint16_t* __restrict__ lut16, int pivot,
     int n1, uint8_t* __restrict__ bp, int32_t* __restrict__ send, int32_t* __restrict__ ovbuf,
     uint32_t* __restrict__ flags, int32_t* __restrict__ counter, uint32_t epoch,
-    int spin_limit, uint32_t* __restrict__ err, float one) {
+    int spin_limit, uint32_t* __restrict__ err) {
     using G = Geom<K>;
     __shared__ FwdSmem<K, 1> sm;
     __shared__ int32_t task, cur;
@@ -745,7 +709,7 @@ __global__ __launch_bounds__(kFwdThreads) void tailbite_fused_kernel(
     if (t < nseq) {
         if (tid == 0) sm.ovs[0] = -1;
         fwd_run<K, 1>(sm, X, kSteps, kSteps, t, 1, lut16, pivot, n1, pivot, false, bp, &cur,
-                      err, one, tid);
+                      err, tid);
         // This workgroup's backpointer stores reach L2 (and are written back
         // past it, since pass 2 of this sequence may run on another XCD and
         // overwrite them) before any thread reads them back.
@@ -779,7 +743,7 @@ __global__ __launch_bounds__(kFwdThreads) void tailbite_fused_kernel(
         __syncthreads();
         if (sm.ovs[0] < 0) return;             // wait expired: reported through err
         fwd_run<K, 1>(sm, X, kSteps, kSteps, q, 1, lut16, 0, kSteps, 0, true, bp, send + q,
-                      err, one, tid);
+                      err, tid);
     }
 }
 
@@ -915,7 +879,7 @@ __global__ __launch_bounds__(kFwdThreads) void ldlq_chain_kernel(
     float* __restrict__ xbuf, float* __restrict__ hatW, float* __restrict__ Eq,
     int32_t* __restrict__ states, int16_t* __restrict__ trellis, uint32_t* __restrict__ flags,
     int32_t* __restrict__ counter, uint32_t epoch, int spin_limit, uint32_t* __restrict__ err,
-    int xdump, float one) {
+    int xdump) {
     using G = Geom<K>;
     __shared__ FwdSmem<K, 1> sm;
     __shared__ float part[kFwdThreads / 64][256];     // per-wave feedback partials
@@ -1071,7 +1035,7 @@ __global__ __launch_bounds__(kFwdThreads) void ldlq_chain_kernel(
             asm volatile("" : "+v"(tidv));
             asm volatile("" : "+s"(lutv));
             fwd_run<K, 1>(sm, xs, kSteps, kSteps, 0, 1, lutv, pass ? 0 : pivot, nst, lo,
-                          pass != 0, bpw, &cur, err, one, tidv);
+                          pass != 0, bpw, &cur, err, tidv);
             // the backpointers are read back by this workgroup only: the
             // barrier's workgroup-scope ordering suffices
             __syncthreads();
@@ -1140,22 +1104,22 @@ struct FwdL {
         if (T == 1)
             hipLaunchKernelGGL((fwd_kernel<K, 1>), dim3(nwg), dim3(kFwdThreads), 0, s, X,
                                xstride, xlen, nseq, lut16, roll, nsteps, store_lo, ov_in,
-                               (uint8_t*)bp, send, err, 1.0f);
+                               (uint8_t*)bp, send, err);
         else if constexpr (max_group<K>() >= 2) {
             if (T == 2)
                 hipLaunchKernelGGL((fwd_kernel<K, 2>), dim3(nwg), dim3(kFwdThreads), 0, s,
                                    X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo,
                                    ov_in,
-                                   (uint8_t*)bp, send, err, 1.0f);
+                                   (uint8_t*)bp, send, err);
             else if constexpr (max_group<K>() >= 4) {
                 if (T == 4)
                     hipLaunchKernelGGL((fwd_kernel<K, 4>), dim3(nwg), dim3(kFwdThreads), 0, s,
                                        X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo,
-                                       ov_in, (uint8_t*)bp, send, err, 1.0f);
+                                       ov_in, (uint8_t*)bp, send, err);
                 else if constexpr (max_group<K>() >= 8)
                     hipLaunchKernelGGL((fwd_kernel<K, 8>), dim3(nwg), dim3(kFwdThreads), 0, s,
                                        X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo,
-                                       ov_in, (uint8_t*)bp, send, err, 1.0f);
+                                       ov_in, (uint8_t*)bp, send, err);
             }
         }
         return hipGetLastError();
@@ -1196,7 +1160,7 @@ struct FusedL {
         hipLaunchKernelGGL(reset_counter_kernel, dim3(1), dim3(1), 0, s, counter);
         hipLaunchKernelGGL(tailbite_fused_kernel<K>, dim3(2 * nseq), dim3(kFwdThreads), 0, s,
                            X, nseq, lut16, pivot, n1, (uint8_t*)bp, send, ovbuf, flags,
-                           counter, epoch, spin_limit, err, 1.0f);
+                           counter, epoch, spin_limit, err);
         return hipGetLastError();
     }
 };
@@ -1211,7 +1175,7 @@ struct ChainL {
         hipLaunchKernelGGL(reset_counter_kernel, dim3(1), dim3(1), 0, s, counter);
         hipLaunchKernelGGL(ldlq_chain_kernel<K>, dim3(nwg), dim3(kFwdThreads), 0, s, W, Lq, k,
                            n, jc0, tnl, lut16, pivot, n1, (uint8_t*)bp, xbuf, hatW, Eq, states,
-                           trellis, flags, counter, epoch, spin_limit, err, xdump, 1.0f);
+                           trellis, flags, counter, epoch, spin_limit, err, xdump);
         return hipGetLastError();
     }
 };
