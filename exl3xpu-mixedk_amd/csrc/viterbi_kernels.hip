@@ -171,12 +171,15 @@ __device__ __forceinline__ int bp_lookup(const uint8_t* row, int j) {
 template <int K, int T>
 constexpr bool kGroupOps = (K >= 6) || (K == 5 && T >= 2);
 
-// Candidates per chunk of the min tree: 16, or 8 for K=5 at T >= 2 and for
-// K=7 at T = 1, where the smaller chunk's keys make room for the fp32
-// codebook registers (16-wide chunks spilled there: K=5 batched 285k ->
-// 367k tiles/s, the K=7 column chain 0.42 -> 0.36 s with 8).
+// Candidates per chunk of the min tree: 8 wherever the smaller chunk's keys
+// make room for the fp32 codebook registers -- every K at T = 1 (the column
+// chain) and K <= 5 at any T (16-wide chunks spilled there: K=5 batched
+// 285k -> 367k tiles/s, K=4 batched 346k -> 361k, the 5120x5120 column
+// chain at K=4/5/6/7 0.355/0.366/0.350/0.42 s -> 0.336/0.345/0.340/0.358 s);
+// 16 for K = 6, 7 at T >= 2, where 8 measured 2 % and 1 % slower.
 template <int K, int T>
-constexpr int kChunkW = ((K == 5 && T >= 2) || (K == 7 && T == 1)) ? 8 : Geom<K>::NCH;
+constexpr int kChunkW =
+    (T == 1 || K <= 5) ? (Geom<K>::NCH < 8 ? Geom<K>::NCH : 8) : Geom<K>::NCH;
 
 // Shared memory of one forward run over T sequences.
 template <int K, int T>
