@@ -434,11 +434,11 @@ int run_tailbite(DevCtx& cx, const float* dX, int nseq, int K, Code code, int ma
     return scratch_end(cx, s, sync);
 }
 
-// Relative cost of one tile of the chain kernel per K (whole-tensor times
-// of the 5120x5120 sweep: 0.409 / 0.348 / 0.357 / 0.368 / 0.351 / 0.359 s
-// for K = 2..7), for splitting the CUs between groups.
+// Relative cost of one tile of the chain kernel per K (kernel times of the
+// 5120x5120 sweep: 385 / 328 / 317 / 326 / 321 / 339 ms for K = 2..7), for
+// splitting the CUs between groups.
 double chain_tile_cost(int K) {
-    static const double c[8] = {1.0, 1.0, 1.15, 0.97, 1.0, 1.03, 0.98, 1.01};
+    static const double c[8] = {1.0, 1.0, 1.21, 1.03, 1.0, 1.03, 1.01, 1.07};
     return (K >= 2 && K <= 7) ? c[K] : 1.0;
 }
 
