@@ -188,12 +188,17 @@ constexpr int kChunkW =
 // Each wave is raised to kPrioTop<K> after the barrier and lowered as it
 // passes fixed points of its step's work, so that waves ahead yield the
 // SIMD to those behind and all arrive together.  Points, in units of
-// (sequence, chunk, group) of the step: K >= 4 drop to 1 at half and to 0
-// at three quarters, K = 3 to 0 at three quarters, K = 2 (one chunk of
-// 4-candidate groups) to 0 right after the step's target is read.  Measured
-// against no priorities (same box, alternating runs): batched K = 2..7
-// 256k/339k/360k/364k/358k/352k -> 311k/371k/391k/392k/391k/390k tiles/s,
-// the 5120x5120 column chain at K = 2..7 -10/-3/-3/-9/-7/-7 %.
+// (sequence, chunk, group) of the step: K >= 5 drop to 1 at 5/8 and to 0 at
+// 7/8, K = 4 to 1 at half and to 0 at three quarters, K = 3 to 0 at three
+// quarters, K = 2 (one chunk of 4-candidate groups) to 0 right after the
+// step's target is read.  Measured against no priorities (same box,
+// alternating runs): batched K = 2..7 256k/339k/360k/364k/358k/352k ->
+// 311k/371k/391k/392k/391k/390k tiles/s with K >= 5 on the K = 4 points,
+// which K >= 5's own add 1 % to (and 2.5 % to their column chain, where
+// K = 4 loses 2 % with them); the 5120x5120 column chain at K = 2..7
+// -10/-3/-3/-11/-9/-9 %.  Slower: later drops for K = 2 (294k at three
+// quarters), other points or a third level for K = 3, a fourth level for
+// K >= 4.
 template <int K>
 constexpr int kPrioTop = K >= 4 ? 2 : 1;
 
@@ -311,9 +316,9 @@ __device__ __forceinline__ void fwd_run(
                         constexpr int U = T * NCHUNK * G::C;  // units of a step
                         const int pos = (tt * NCHUNK + qc) * G::C + c;
                         if constexpr (K >= 4) {
-                            if (pos == U / 2) __builtin_amdgcn_s_setprio(1);
+                            if (pos == (K >= 5 ? U * 5 / 8 : U / 2)) __builtin_amdgcn_s_setprio(1);
                         }
-                        if (pos == U * 3 / 4) __builtin_amdgcn_s_setprio(0);
+                        if (pos == (K >= 5 ? U * 7 / 8 : U * 3 / 4)) __builtin_amdgcn_s_setprio(0);
                     }
                     double kk[NCH];
                     if constexpr (kGroupOps<K, T>) {
