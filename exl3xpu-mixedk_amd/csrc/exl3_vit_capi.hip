@@ -434,11 +434,13 @@ int run_tailbite(DevCtx& cx, const float* dX, int nseq, int K, Code code, int ma
     return scratch_end(cx, s, sync);
 }
 
-// Relative cost of one tile of the chain kernel per K (kernel times of the
-// 5120x5120 sweep: 385 / 328 / 317 / 326 / 321 / 339 ms for K = 2..7), for
-// splitting the CUs between groups.
+// Relative cost of one tile of the chain kernel per K, for splitting the CUs
+// between groups: kernel times of the 5120x5120 sweep (344 / 319 / 309 /
+// 290 / 289 / 309 ms for K = 2..7), K = 7 raised by 2 % to the K=7 : K=5
+// ratio measured with both running side by side (c4's q at K=5, k and v at
+// K=7).
 double chain_tile_cost(int K) {
-    static const double c[8] = {1.0, 1.0, 1.21, 1.03, 1.0, 1.03, 1.01, 1.07};
+    static const double c[8] = {1.0, 1.0, 1.11, 1.03, 1.0, 0.94, 0.94, 1.02};
     return (K >= 2 && K <= 7) ? c[K] : 1.0;
 }
 
