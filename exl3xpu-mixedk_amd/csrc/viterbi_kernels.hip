@@ -173,13 +173,14 @@ constexpr bool kGroupOps = (K >= 6) || (K == 5 && T >= 2);
 
 // Candidates per chunk of the min tree: 8 wherever the smaller chunk's keys
 // make room for the fp32 codebook registers -- every K at T = 1 (the column
-// chain) and K <= 5 at any T (16-wide chunks spilled there: K=5 batched
+// chain) and K != 6 at any T (16-wide chunks spilled there: K=5 batched
 // 285k -> 367k tiles/s, K=4 batched 346k -> 361k, the 5120x5120 column
-// chain at K=4/5/6/7 0.355/0.366/0.350/0.42 s -> 0.336/0.345/0.340/0.358 s);
-// 16 for K = 6, 7 at T >= 2, where 8 measured 2 % and 1 % slower.
+// chain at K=4/5/6/7 0.355/0.366/0.350/0.42 s -> 0.336/0.345/0.340/0.358 s,
+// K=7 batched +1 % with the wave priorities below); 16 for K = 6 at T >= 2,
+// where 8 measured 2 % slower.
 template <int K, int T>
 constexpr int kChunkW =
-    (T == 1 || K <= 5) ? (Geom<K>::NCH < 8 ? Geom<K>::NCH : 8) : Geom<K>::NCH;
+    (T == 1 || K != 6) ? (Geom<K>::NCH < 8 ? Geom<K>::NCH : 8) : Geom<K>::NCH;
 
 // Wave priorities within a step (s_setprio).  All 16 waves meet at the
 // step's barrier, and the SIMD's arbiter otherwise serves its oldest wave
