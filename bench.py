@@ -379,10 +379,14 @@ def main():
     ap.add_argument("--no-k-sweep", action="store_true", help="skip the K = 2..7 sweep")
     ap.add_argument("--configs", default="c1,c2,c3,c4,c5",
                     help="comma-separated end-to-end workloads to run (empty: none)")
+    ap.add_argument("--schedule", choices=xq.SCHEDULES, default=xq.DEFAULT_SCHEDULE,
+                    help="BlockLDLQ launch schedule of the end-to-end configs (auto: one "
+                         "persistent column-chain launch per weight on the GPU)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="after the timed steps, copy a buffer of BYTES bytes three times "
                          "(a known-traffic kernel for scaling HBM counters)")
     args = ap.parse_args()
+    xq.DEFAULT_SCHEDULE = args.schedule
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; multi-GPU runs are out of scope "
               "(the encoder shards by output-column tile chains, one process per GPU)",
