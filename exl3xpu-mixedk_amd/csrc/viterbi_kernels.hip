@@ -190,7 +190,8 @@ constexpr int kChunkW =
 // passes fixed points of its step's work, so that waves ahead yield the
 // SIMD to those behind and all arrive together.  Points, in units of
 // (sequence, chunk, group) of the step: K >= 5 drop to 1 at 5/8 and to 0 at
-// 7/8, K = 4 to 1 at half and to 0 at three quarters, K = 3 to 0 at three
+// 7/8, K = 4 to 1 at half and to 0 at three quarters (at 1/4 and 5/8 for a
+// single sequence, the column chain: -1 % there), K = 3 to 0 at three
 // quarters, K = 2 (one chunk of 4-candidate groups) to 0 right after the
 // step's target is read.  Measured against no priorities (same box,
 // alternating runs): batched K = 2..7 256k/339k/360k/364k/358k/352k ->
@@ -316,10 +317,14 @@ __device__ __forceinline__ void fwd_run(
                     if constexpr (K >= 3) {
                         constexpr int U = T * NCHUNK * G::C;  // units of a step
                         const int pos = (tt * NCHUNK + qc) * G::C + c;
+                        // drop points, as fractions of the step's units
+                        constexpr int D1 = K >= 5 ? U * 5 / 8 : T == 1 ? U / 4 : U / 2;
+                        constexpr int D0 = K >= 5 ? U * 7 / 8 : K == 4 && T == 1 ? U * 5 / 8
+                                                                                  : U * 3 / 4;
                         if constexpr (K >= 4) {
-                            if (pos == (K >= 5 ? U * 5 / 8 : U / 2)) __builtin_amdgcn_s_setprio(1);
+                            if (pos == D1) __builtin_amdgcn_s_setprio(1);
                         }
-                        if (pos == (K >= 5 ? U * 7 / 8 : U * 3 / 4)) __builtin_amdgcn_s_setprio(0);
+                        if (pos == D0) __builtin_amdgcn_s_setprio(0);
                     }
                     double kk[NCH];
                     if constexpr (kGroupOps<K, T>) {
