@@ -192,8 +192,9 @@ constexpr int kChunkW =
 // (sequence, chunk, group) of the step: K >= 5 drop to 1 at 5/8 and to 0 at
 // 7/8, K = 4 to 1 at half and to 0 at three quarters (at 1/4 and 5/8 for a
 // single sequence, the column chain: -1 % there), K = 3 to 0 at three
-// quarters, K = 2 (one chunk of 4-candidate groups) to 0 right after the
-// step's target is read.  Measured against no priorities (same box,
+// quarters, K = 2 (one chunk of 4-candidate groups) to 1 right after the
+// step's target is read and to 0 after a quarter of its groups (the column
+// chain -3 % against dropping to 0 at the target read).  Measured against no priorities (same box,
 // alternating runs): batched K = 2..7 256k/339k/360k/364k/358k/352k ->
 // 311k/371k/391k/392k/391k/390k tiles/s with K >= 5 on the K = 4 points,
 // which K >= 5's own add 1 % to (and 2.5 % to their column chain, where
@@ -202,7 +203,7 @@ constexpr int kChunkW =
 // quarters), other points or a third level for K = 3, a fourth level for
 // K >= 4.
 template <int K>
-constexpr int kPrioTop = K >= 4 ? 2 : 1;
+constexpr int kPrioTop = K == 3 ? 1 : 2;
 
 // Shared memory of one forward run over T sequences.
 template <int K, int T>
@@ -294,7 +295,7 @@ __device__ __forceinline__ void fwd_run(
             const int q = q0 + tt;
             const float negx = -__int_as_float(
                 __builtin_amdgcn_readfirstlane(__float_as_int(xs[tt][u])));
-            if constexpr (K == 2) __builtin_amdgcn_s_setprio(0);
+            if constexpr (K == 2) __builtin_amdgcn_s_setprio(1);
             const float* bcur = bbuf[tt][i & 1];
 
             double run[G::C];
@@ -314,6 +315,9 @@ __device__ __forceinline__ void fwd_run(
 #pragma unroll
                 for (int c = 0; c < G::C; ++c) {
                     const int blk = c / G::CB;
+                    if constexpr (K == 2) {
+                        if (c == G::C / 4) __builtin_amdgcn_s_setprio(0);
+                    }
                     if constexpr (K >= 3) {
                         constexpr int U = T * NCHUNK * G::C;  // units of a step
                         const int pos = (tt * NCHUNK + qc) * G::C + c;
