@@ -166,10 +166,11 @@ __device__ __forceinline__ int bp_lookup(const uint8_t* row, int j) {
 
 // --------------------------------------------------------------- forward DP
 // Whether the candidate arithmetic is issued grouped by opcode (see fwd_run):
-// measured faster for K >= 6, and for K = 5 with T >= 2 sequences per
-// workgroup; at T = 1 (the column chain) K = 5 is 3 % faster ungrouped.
+// measured faster for K >= 6, and for K = 4, 5 with T >= 2 sequences per
+// workgroup (K=4 +1.6 % with the wave priorities below); at T = 1 (the
+// column chain) K = 4 and 5 are 1-3 % faster ungrouped.
 template <int K, int T>
-constexpr bool kGroupOps = (K >= 6) || (K == 5 && T >= 2);
+constexpr bool kGroupOps = (K >= 6) || ((K == 4 || K == 5) && T >= 2);
 
 // Candidates per chunk of the min tree: 8 wherever the smaller chunk's keys
 // make room for the fp32 codebook registers -- every K at T = 1 (the column
@@ -353,7 +354,7 @@ __device__ __forceinline__ void fwd_run(
                         for (int w = 0; w < NCH; ++w)
                             kk[w] = key_of(tag[w], dv[w] + B[blk][w]);
                     } else {
-                        // K <= 4, and K = 5 at T = 1: the compiler's own
+                        // K <= 3, and K = 4, 5 at T = 1: the compiler's own
                         // interleaving measures faster.
 #pragma unroll
                         for (int w = 0; w < NCH; ++w) {
