@@ -25,7 +25,8 @@
  *   argmin    lowest state index among equal minima            quantize.py:306,315
  *   backtrace s_{i-1} = (s_i >> K) + bp_i[s_i >> K] * SP       quantize.py:316-319
  *
- * Build: see oracle/Makefile (gcc -O2 -ffp-contract=off, no fast-math).
+ * Build: see oracle/Makefile (gcc -O3 -mavx2 -ffp-contract=off, no fast-math:
+ * vectorised, but every element sees the same IEEE fp32 operations).
  */
 #include <math.h>
 #include <stdint.h>
@@ -40,6 +41,75 @@
 #define ORC_EARG 1
 #define ORC_ENOMEM 2
 
+/*
+ * One DP step: bn[j] = b_i[j] = min_w c_{i-1}[j + w*SP] and bw[j] = the
+ * first w attaining it, where
+ *   c_{i-1}[s] = fl(fl(fl(lut[s] - xp)^2) + b[s >> K])
+ * and (j + w*SP) >> K = (j >> K) + w*Q; the first w wins ties (ascending w,
+ * only a strictly smaller cost replaces).  Blocks of groups stay in L1; the
+ * innermost loop runs over the NC groups sharing one predecessor minimum,
+ * so it vectorises with that minimum broadcast.  dp_step_k is instantiated
+ * for K >= 4 so the innermost trip count is a constant.
+ */
+static inline __attribute__((always_inline)) void
+dp_step_k(const int K, const int L, const float *lut, const float *b, float xp,
+          float *bn, int32_t *bw)
+{
+    const int NC = 1 << K, SP = 1 << (L - K), Q = SP >> K;
+    enum { JB = 256 };
+    for (int j0 = 0; j0 < SP; j0 += JB) {
+        const int jn = SP - j0 < JB ? SP - j0 : JB;
+        float *bb = bn + j0;
+        int32_t *ww = bw + j0;
+        for (int a = 0; a < (jn >> K); ++a) {       /* w = 0 */
+            const float pb = b[(j0 >> K) + a];
+            const float *lw = lut + j0 + (a << K);
+            for (int r = 0; r < NC; ++r) {
+                float d = lw[r] - xp;
+                float e = d * d;
+                bb[(a << K) + r] = e + pb;
+                ww[(a << K) + r] = 0;
+            }
+        }
+        for (int w = 1; w < NC; ++w) {
+            const float *lw = lut + (size_t)w * SP + j0;
+            const float *bp = b + (size_t)w * Q + (j0 >> K);
+            for (int a = 0; a < (jn >> K); ++a) {
+                const float pb = bp[a];
+                float *bq = bb + (a << K);
+                int32_t *wq = ww + (a << K);
+                const float *lq = lw + (a << K);
+                for (int r = 0; r < NC; ++r) {
+                    float d = lq[r] - xp;
+                    float e = d * d;
+                    float v = e + pb;
+                    const int lt = v < bq[r];
+                    bq[r] = lt ? v : bq[r];
+                    wq[r] = lt ? w : wq[r];
+                }
+            }
+        }
+    }
+}
+
+static void dp_step(int K, int L, const float *lut, const float *b, float xp,
+                    float *bn, int32_t *bw)
+{
+    if (L == 16) {
+        switch (K) {
+        case 4: dp_step_k(4, 16, lut, b, xp, bn, bw); return;
+        case 5: dp_step_k(5, 16, lut, b, xp, bn, bw); return;
+        case 6: dp_step_k(6, 16, lut, b, xp, bn, bw); return;
+        case 7: dp_step_k(7, 16, lut, b, xp, bn, bw); return;
+        case 8: dp_step_k(8, 16, lut, b, xp, bn, bw); return;
+        default: break;
+        }
+    }
+    /* K = 2, 3 (their short innermost loops vectorise better with a
+     * run-time trip count) and the small test trellises */
+    dp_step_k(K, L, lut, b, xp, bn, bw);
+}
+
 /* ---------------------------------------------------------------- one run */
 /*
  * One Viterbi run over x[0..T-1] on the 2^L-state shift-register trellis,
@@ -53,48 +123,42 @@
  */
 static int viterbi_run(const float *x, int T, const float *lut, int K, int L,
                        int overlap, int back_from, int32_t *states,
-                       float *cost, float *best, uint8_t *from_state)
+                       float *cost, float *best, int32_t *bw, uint8_t *from_state)
 {
-    const int S = 1 << L, NC = 1 << K, SP = 1 << (L - K);
+    const int S = 1 << L, SP = 1 << (L - K);
     const float INF = INFINITY;
-    float x0 = x[0];
-    for (int s = 0; s < S; ++s) {
-        float d = lut[s] - x0;
-        float e = d * d;
-        if (overlap >= 0)
-            e = e + (((s >> K) == overlap) ? 0.0f : INF);
-        cost[s] = e;
-    }
+    /* b holds the group minima b_i (SP floats), cost doubles as the buffer
+     * of b_{i+1} while it is being formed, and finally holds c_{T-1}.
+     * b_0 is the start mask: 0 (free) or 0 / +inf (pinned to overlap), so
+     * c_0[s] = fl(e_0[s] + b_0[s >> K]) is e_0[s] or +inf, as the
+     * reference's e + m (quantize.py:264-270). */
+    float *b = best, *bn = cost;
+    for (int g = 0; g < SP; ++g)
+        b[g] = (overlap < 0 || g == overlap) ? 0.0f : INF;
     for (int i = 1; i < T; ++i) {
         int keep = (back_from < 0) || (i > back_from);
         uint8_t *fs = NULL;
         if (keep)
             fs = from_state + (size_t)(back_from < 0 ? i : i - 1 - back_from) * SP;
-        for (int j = 0; j < SP; ++j) {
-            float bv = cost[j];
-            int bw = 0;
-            for (int w = 1; w < NC; ++w) {
-                float v = cost[j + w * SP];
-                if (v < bv) { bv = v; bw = w; }
-            }
-            best[j] = bv;
-            if (fs) fs[j] = (uint8_t)bw;
-        }
-        float xi = x[i];
-        for (int s = 0; s < S; ++s) {
-            float d = lut[s] - xi;
-            float e = d * d;
-            cost[s] = e + best[s >> K];
-        }
+        const float xp = x[i - 1];
+        dp_step(K, L, lut, b, xp, bn, bw);
+        if (fs)
+            for (int j = 0; j < SP; ++j) fs[j] = (uint8_t)bw[j];
+        float *t = b; b = bn; bn = t;
     }
-    if (overlap >= 0) {
-        for (int s = 0; s < S; ++s)
-            cost[s] = cost[s] + (((s & (SP - 1)) == overlap) ? 0.0f : INF);
-    }
+    /* c_{T-1}[s] = fl(e_{T-1}[s] + b_{T-1}[s >> K]) (+ the pinned end mask,
+     * quantize.py:298-303), then the lowest index among the minima. */
+    const float xl = x[T - 1];
     int am = 0;
-    float mv = cost[0];
-    for (int s = 1; s < S; ++s)
-        if (cost[s] < mv) { mv = cost[s]; am = s; }
+    float mv = 0.0f;
+    for (int s = 0; s < S; ++s) {
+        float d = lut[s] - xl;
+        float e = d * d;
+        float v = e + b[s >> K];
+        if (overlap >= 0)
+            v = v + (((s & (SP - 1)) == overlap) ? 0.0f : INF);
+        if (s == 0 || v < mv) { mv = v; am = s; }
+    }
     if (back_from >= 0) {
         int s = am;
         for (int i = T - 1; i > back_from; --i) {
@@ -122,22 +186,23 @@ static int check_args(int T, int K, int L)
 }
 
 /* Scratch for one sequence: cost S + best SP floats, from_state T*SP bytes. */
-typedef struct { float *cost, *best; uint8_t *fs; int32_t *tmp; } scratch_t;
+typedef struct { float *cost, *best; int32_t *bw; uint8_t *fs; int32_t *tmp; } scratch_t;
 
 static int scratch_alloc(scratch_t *w, int T, int L, int K)
 {
     const int S = 1 << L, SP = 1 << (L - K);
     w->cost = (float *)malloc(sizeof(float) * S);
     w->best = (float *)malloc(sizeof(float) * SP);
+    w->bw = (int32_t *)malloc(sizeof(int32_t) * SP);
     w->fs = (uint8_t *)malloc((size_t)T * SP);
     w->tmp = (int32_t *)malloc(sizeof(int32_t) * T);
-    if (!w->cost || !w->best || !w->fs || !w->tmp) return ORC_ENOMEM;
+    if (!w->cost || !w->best || !w->bw || !w->fs || !w->tmp) return ORC_ENOMEM;
     return ORC_OK;
 }
 
 static void scratch_free(scratch_t *w)
 {
-    free(w->cost); free(w->best); free(w->fs); free(w->tmp);
+    free(w->cost); free(w->best); free(w->bw); free(w->fs); free(w->tmp);
 }
 
 /*
@@ -168,7 +233,7 @@ int orc_viterbi(const float *X, int nseq, int T, const float *lut, int K, int L,
                 int ov = overlap ? overlap[q] : -1;
                 int32_t *o = back_from >= 0 ? out + q : out + (size_t)q * T;
                 viterbi_run(X + (size_t)q * T, T, lut, K, L, ov, back_from, o,
-                            w.cost, w.best, w.fs);
+                            w.cost, w.best, w.bw, w.fs);
             }
         }
         scratch_free(&w);
@@ -214,17 +279,17 @@ int orc_tailbite(const float *X, int nseq, int T, const float *lut, int K,
                 if (margin > 0 && pivot + margin < T) {
                     int32_t sp1;
                     viterbi_run(roll, pivot + margin, lut, K, L, -1, pivot,
-                                &sp1, w.cost, w.best, w.fs);
+                                &sp1, w.cost, w.best, w.bw, w.fs);
                     s_p = sp1;
                 } else {
                     viterbi_run(roll, T, lut, K, L, -1, -1, w.tmp, w.cost,
-                                w.best, w.fs);
+                                w.best, w.bw, w.fs);
                     s_p = w.tmp[pivot];
                 }
                 int ov = s_p >> K;
                 if (ov_out) ov_out[q] = ov;
                 viterbi_run(x, T, lut, K, L, ov, -1, out + (size_t)q * T,
-                            w.cost, w.best, w.fs);
+                            w.cost, w.best, w.bw, w.fs);
             }
         }
         free(roll);
