@@ -157,17 +157,35 @@ void prof_collect() {
     }
     g_prof_pending.clear();
 }
-bool g_env_read = false;
-long long g_maxseq = 1LL << 24;
+// Bounds and budgets from the environment, read on every call (as the
+// reference does, viterbi_esimd.cpp:924-933), so a caller may change them
+// between calls.
+//   host-pointer entries (xtq_vit_run, xtq_vit_run_k), the reference's
+//   bounds and defaults:
+//     XTQ_VIT_MAXSEQ    nseq per call (default 4096)            -> status 6
+//     XTQ_VIT_MAXBYTES  nseq * 1,317,888 B, the reference's worst-case
+//                       device bytes per sequence (default 6 GiB) -> status 5
+//   every entry:
+//     XTQ_VIT_DEV_MAXBYTES  library-owned device bytes (default 64 GiB)
+//                       -> status 5
+//     XTQ_VIT_SCRATCH   backpointer scratch budget; larger batches run in
+//                       chunks (default 8 GiB)
+long long g_host_maxseq = 4096;
+size_t g_host_maxbytes = (size_t)6 << 30;
 size_t g_maxbytes = (size_t)64 << 30;
 size_t g_scratch = (size_t)8 << 30;
+// Worst-case device bytes per sequence of the reference's library (X 1 KiB,
+// states 1 KiB, cost table 256 KiB, backpointers 1 MiB).
+constexpr size_t kRefBytesPerSeq = 1317888;
 
 void read_env() {
-    if (g_env_read) return;
-    if (const char* e = getenv("XTQ_VIT_MAXSEQ")) g_maxseq = atoll(e);
-    if (const char* e = getenv("XTQ_VIT_MAXBYTES")) g_maxbytes = strtoull(e, nullptr, 10);
-    if (const char* e = getenv("XTQ_VIT_SCRATCH")) g_scratch = strtoull(e, nullptr, 10);
-    g_env_read = true;
+    const char* e;
+    g_host_maxseq = (e = getenv("XTQ_VIT_MAXSEQ")) ? atoll(e) : 4096;
+    g_host_maxbytes = (e = getenv("XTQ_VIT_MAXBYTES")) ? strtoull(e, nullptr, 10)
+                                                       : (size_t)6 << 30;
+    g_maxbytes = (e = getenv("XTQ_VIT_DEV_MAXBYTES")) ? strtoull(e, nullptr, 10)
+                                                      : (size_t)64 << 30;
+    g_scratch = (e = getenv("XTQ_VIT_SCRATCH")) ? strtoull(e, nullptr, 10) : (size_t)8 << 30;
 }
 
 // Makes `dev` ready on the calling thread (which must have it current).
@@ -239,11 +257,8 @@ int grow(P** p, size_t* cap, size_t want, size_t elem, size_t* owned) {
     return 0;
 }
 
-int check_common(int nseq, int K, int margin, int pivot) {
-    if (nseq <= 0 || nseq > g_maxseq) {
-        fprintf(stderr, "xtq_vit: nseq %d out of range (XTQ_VIT_MAXSEQ %lld)\n", nseq, g_maxseq);
-        return 6;
-    }
+// K, pivot and margin of a tail-bite call.
+int check_args(int K, int margin, int pivot) {
     if (K < 2 || K > 7) return 9;
     if (pivot < 0 || pivot >= xtq::kSteps || margin < 0) return 10;
     return 0;
@@ -273,7 +288,7 @@ int reserve_scratch(DevCtx& cx, int K, int chunk) {
     if ((size_t)chunk * per > cx.bp_cap) add += (size_t)chunk * per - cx.bp_cap;
     if ((size_t)chunk > cx.seq_cap) add += ((size_t)chunk - cx.seq_cap) * 3 * sizeof(int32_t);
     if (cx.owned + add > g_maxbytes) {
-        fprintf(stderr, "xtq_vit: request over XTQ_VIT_MAXBYTES (%zu)\n", g_maxbytes);
+        fprintf(stderr, "xtq_vit: request over XTQ_VIT_DEV_MAXBYTES (%zu)\n", g_maxbytes);
         return 5;
     }
     size_t bpcap_bytes = cx.bp_cap;
@@ -363,34 +378,44 @@ bool use_lanes(int n) {
 // seconds; a pass-1 task takes about a millisecond).
 constexpr int kSpinLimit = 1 << 22;
 
-// The two-pass tail-biting schedule over device buffers (quantize.py:323-354).
-int run_tailbite(DevCtx& cx, const float* dX, int nseq, int K, Code code, int margin,
-                 int pivot, int32_t* d_states, int16_t* d_trellis, hipStream_t s,
-                 bool sync = true) {
-    const int chunk = chunk_size(cx, K, nseq);
-    int rc = reserve_scratch(cx, K, chunk);
-    if (!rc) rc = scratch_begin(cx, s);
-    if (rc) return rc;
+// Device scratch of one tail-bite call: backpointer slots (bp_tile_bytes(K)
+// per sequence of a chunk), per-sequence final state / pass-1 pin / fused
+// ready flag, the fused kernel's task counter and the status word.
+struct TbScratch {
+    void* bp;
+    int32_t* send;
+    int32_t* ov;
+    uint32_t* flags;
+    int32_t* counter;
+    uint32_t* err;
+};
+
+// The two-pass tail-biting schedule (quantize.py:323-354) over chunks of
+// `chunk` sequences, enqueued on s with the buffers in w.  prof: bracket the
+// launches with timing events (the benchmark's kernel timing).
+int tailbite_chunks(DevCtx& cx, const TbScratch& w, int chunk, const float* dX, int nseq,
+                    int K, Code code, int margin, int pivot, int32_t* d_states,
+                    int16_t* d_trellis, hipStream_t s, bool prof) {
     const int n1 = (margin > 0 && pivot + margin < xtq::kSteps) ? pivot + margin : xtq::kSteps;
     const uint16_t* lut = cx.lut16[code];
+    auto pbeg = [&](int kind, double steps) { return prof ? prof_begin(s, kind, steps) : -1; };
     for (int c0 = 0; c0 < nseq; c0 += chunk) {
         const int n = (nseq - c0) < chunk ? (nseq - c0) : chunk;
         const float* x = dX + (size_t)c0 * xtq::kSteps;
+        int32_t* st = d_states ? d_states + (size_t)c0 * xtq::kSteps : nullptr;
+        int16_t* tr = d_trellis ? d_trellis + (size_t)c0 * 16 * K : nullptr;
         const int T = pick_group(cx, K, n);
         hipError_t e;
         if (use_fused(cx, n)) {
             if (++cx.epoch == 0) cx.epoch = 1;
-            int pf = prof_begin(s, 0, (double)n * (n1 + xtq::kSteps));
-            e = xtq::launch_tailbite_fused(K, x, n, lut, pivot, n1, cx.bp, cx.send, cx.ov,
-                                           cx.flags, cx.counter, cx.epoch, kSpinLimit, cx.err,
-                                           s);
+            int pf = pbeg(0, (double)n * (n1 + xtq::kSteps));
+            e = xtq::launch_tailbite_fused(K, x, n, lut, pivot, n1, w.bp, w.send, w.ov, w.flags,
+                                           w.counter, cx.epoch, kSpinLimit, w.err, s);
             prof_end(pf, s);
             if (e == hipSuccess) {
-                pf = prof_begin(s, 1, 0.0);
-                e = xtq::launch_traceback(
-                    K, cx.bp, n, cx.send, xtq::kSteps, 0, 0, nullptr,
-                    d_states ? d_states + (size_t)c0 * xtq::kSteps : nullptr,
-                    d_trellis ? d_trellis + (size_t)c0 * 16 * K : nullptr, use_lanes(n), s);
+                pf = pbeg(1, 0.0);
+                e = xtq::launch_traceback(K, w.bp, n, w.send, xtq::kSteps, 0, 0, nullptr, st,
+                                          tr, use_lanes(n), s);
                 prof_end(pf, s);
             }
             if (e != hipSuccess) {
@@ -401,29 +426,27 @@ int run_tailbite(DevCtx& cx, const float* dX, int nseq, int K, Code code, int ma
         }
         // Pass 1: free run over the sequence rolled right by pivot, n1 steps,
         // traced back to step pivot: ov = s_pivot >> K.
-        int pf = prof_begin(s, 0, (double)n * n1);
+        int pf = pbeg(0, (double)n * n1);
         e = xtq::launch_forward(K, x, xtq::kSteps, xtq::kSteps, n, lut, pivot, n1, pivot,
-                                nullptr, cx.bp, cx.send, cx.err, T, s);
+                                nullptr, w.bp, w.send, w.err, T, s);
         prof_end(pf, s);
         if (e == hipSuccess) {
-            pf = prof_begin(s, 1, 0.0);
-            e = xtq::launch_traceback(K, cx.bp, n, cx.send, n1, pivot, K, cx.ov, nullptr,
-                                      nullptr, use_lanes(n), s);
+            pf = pbeg(1, 0.0);
+            e = xtq::launch_traceback(K, w.bp, n, w.send, n1, pivot, K, w.ov, nullptr, nullptr,
+                                      use_lanes(n), s);
             prof_end(pf, s);
         }
         // Pass 2: run pinned to ov on the unrolled sequence, full traceback.
         if (e == hipSuccess) {
-            pf = prof_begin(s, 0, (double)n * xtq::kSteps);
+            pf = pbeg(0, (double)n * xtq::kSteps);
             e = xtq::launch_forward(K, x, xtq::kSteps, xtq::kSteps, n, lut, 0, xtq::kSteps, 0,
-                                    cx.ov, cx.bp, cx.send, cx.err, T, s);
+                                    w.ov, w.bp, w.send, w.err, T, s);
             prof_end(pf, s);
         }
         if (e == hipSuccess) {
-            pf = prof_begin(s, 1, 0.0);
-            e = xtq::launch_traceback(
-                K, cx.bp, n, cx.send, xtq::kSteps, 0, 0, nullptr,
-                d_states ? d_states + (size_t)c0 * xtq::kSteps : nullptr,
-                d_trellis ? d_trellis + (size_t)c0 * 16 * K : nullptr, use_lanes(n), s);
+            pf = pbeg(1, 0.0);
+            e = xtq::launch_traceback(K, w.bp, n, w.send, xtq::kSteps, 0, 0, nullptr, st, tr,
+                                      use_lanes(n), s);
             prof_end(pf, s);
         }
         if (e != hipSuccess) {
@@ -431,6 +454,22 @@ int run_tailbite(DevCtx& cx, const float* dX, int nseq, int K, Code code, int ma
             return 4;
         }
     }
+    return 0;
+}
+
+// The tail-bite over the library-owned, grow-only scratch (chunked by the
+// XTQ_VIT_SCRATCH budget).
+int run_tailbite(DevCtx& cx, const float* dX, int nseq, int K, Code code, int margin,
+                 int pivot, int32_t* d_states, int16_t* d_trellis, hipStream_t s,
+                 bool sync = true) {
+    const int chunk = chunk_size(cx, K, nseq);
+    int rc = reserve_scratch(cx, K, chunk);
+    if (!rc) rc = scratch_begin(cx, s);
+    if (rc) return rc;
+    const TbScratch w{cx.bp, cx.send, cx.ov, cx.flags, cx.counter, cx.err};
+    rc = tailbite_chunks(cx, w, chunk, dX, nseq, K, code, margin, pivot, d_states, d_trellis,
+                         s, true);
+    if (rc) return rc;
     return scratch_end(cx, s, sync);
 }
 
@@ -521,7 +560,7 @@ int run_ldlq_chain(DevCtx& cx, const float* W, const float* L, int k, int n,
     if (ntile > cx.cflags_cap) add += (ntile - cx.cflags_cap) * sizeof(uint32_t);
     if (need_x > cx.xbuf_cap) add += (need_x - cx.xbuf_cap) * sizeof(float);
     if (cx.owned + add > g_maxbytes) {
-        fprintf(stderr, "xtq_vit: request over XTQ_VIT_MAXBYTES (%zu)\n", g_maxbytes);
+        fprintf(stderr, "xtq_vit: request over XTQ_VIT_DEV_MAXBYTES (%zu)\n", g_maxbytes);
         return 5;
     }
     if (add && hipEventSynchronize(cx.last) != hipSuccess) return 4;
@@ -622,7 +661,16 @@ int run_host(const float* X, int nseq, int K, Code code, int margin, int pivot,
              int32_t* out) {
     if (!X || !out) return 12;
     read_env();
-    int rc = check_common(nseq, K, margin, pivot);
+    // the reference's bounds, in its order (viterbi_esimd.cpp:973-982)
+    if (nseq <= 0 || nseq > g_host_maxseq) {
+        fprintf(stderr, "xtq_vit: nseq %d over XTQ_VIT_MAXSEQ\n", nseq);
+        return 6;
+    }
+    if ((size_t)nseq * kRefBytesPerSeq > g_host_maxbytes) {
+        fprintf(stderr, "xtq_vit: nseq %d over XTQ_VIT_MAXBYTES\n", nseq);
+        return 5;
+    }
+    int rc = check_args(K, margin, pivot);
     if (rc) return rc;
     int dev = 0, prev = 0;
     rc = host_entry_device(&dev);
@@ -635,7 +683,7 @@ int run_host(const float* X, int nseq, int K, Code code, int margin, int pivot,
         const size_t add = (size_t)nseq > cx.host_cap
                                ? ((size_t)nseq - cx.host_cap) * 2 * xtq::kSteps * 4 : 0;
         if (cx.owned + add > g_maxbytes) {
-            fprintf(stderr, "xtq_vit: nseq %d over XTQ_VIT_MAXBYTES\n", nseq);
+            fprintf(stderr, "xtq_vit: nseq %d over XTQ_VIT_DEV_MAXBYTES\n", nseq);
             rc = 5;
         }
         size_t c1 = cx.host_cap, c2 = cx.host_cap;
@@ -680,8 +728,8 @@ int xtq_vit_init(void) {
         if (hipGetDeviceProperties(&p, dev) == hipSuccess)
             fprintf(stderr, "xtq_vit: device %d %s (%s), %d CUs\n", dev, p.name, p.gcnArchName,
                     p.multiProcessorCount);
-        fprintf(stderr, "xtq_vit: bounds nseq<=%lld devbytes<=%zu scratch=%zu\n", g_maxseq,
-                g_maxbytes, g_scratch);
+        fprintf(stderr, "xtq_vit: bounds nseq<=%lld devbytes<=%zu (library-owned <=%zu, "
+                "scratch %zu)\n", g_host_maxseq, g_host_maxbytes, g_maxbytes, g_scratch);
     }
     if (dev != prev) (void)hipSetDevice(prev);
     return rc;
@@ -699,7 +747,9 @@ int xtq_vit_run(const float* X, int nseq, const char* code, int margin, int pivo
         fprintf(stderr, "xtq_vit: unknown code %s\n", code);
         return 8;
     }
-    return run_host(X, nseq, 4, kMul1, margin, pivot, out);
+    // The reference's kernel runs pass 1 over the whole sequence unless
+    // margin > 0 (viterbi_esimd.cpp:413-414): a negative margin is margin 0.
+    return run_host(X, nseq, 4, kMul1, margin < 0 ? 0 : margin, pivot, out);
 }
 
 int xtq_vit_run_k(const float* X, int nseq, int K, const char* code, int margin, int pivot,
@@ -724,7 +774,8 @@ int tailbite_dev(const float* dX, int nseq, int K, const char* code, int margin,
     int rc = parse_code(code, &c);
     if (rc) return rc;
     read_env();
-    rc = check_common(nseq, K, margin, pivot);
+    if (nseq <= 0) return 6;
+    rc = check_args(K, margin, pivot);
     if (rc) return rc;
     int dev = 0;
     if (current_device(&dev)) return 1;
@@ -789,7 +840,7 @@ int xtq_ldlq_chain_multi_dev(const float* d_W, const float* d_L, int k, int n, i
     if (pivot < 0 || pivot >= xtq::kSteps || margin < 0) return 10;
     if (d_L && ((uintptr_t)d_L & 15)) return 12;     // rows are read as float4
     if (k <= 0 || n <= 0 || k % 16 || n % 16 || col != n ||
-        (long long)(k / 16) * (n / 16) > g_maxseq || k > (1 << 22))
+        (long long)(k / 16) * (n / 16) > INT32_MAX || k > (1 << 22))
         return 6;
     int dev = 0;
     if (current_device(&dev)) return 1;
@@ -808,7 +859,7 @@ int xtq_vit_viterbi_dev(const float* dX, int nseq, int T, int K, const char* cod
     int rc = parse_code(code, &c);
     if (rc) return rc;
     read_env();
-    if (nseq <= 0 || nseq > g_maxseq) return 6;
+    if (nseq <= 0) return 6;
     if (K < 2 || K > 7) return 9;
     if (T < 1 || T > xtq::kSteps || back_from < -1 || back_from >= T) return 10;
     int dev = 0;
@@ -912,8 +963,8 @@ const char* xtq_vit_strerror(int rc) {
         case 2: return "device allocation failed";
         case 3: return "XTQ_VIT_DEVIDX names no device";
         case 4: return "HIP runtime error during a run";
-        case 5: return "request exceeds XTQ_VIT_MAXBYTES";
-        case 6: return "sequence count out of range";
+        case 5: return "request exceeds XTQ_VIT_MAXBYTES or XTQ_VIT_DEV_MAXBYTES";
+        case 6: return "sequence count out of range (XTQ_VIT_MAXSEQ for host pointers)";
         case 8: return "unsupported code";
         case 9: return "unsupported K";
         case 10: return "pivot or margin out of range";

@@ -811,6 +811,7 @@ __global__ __launch_bounds__(kFwdThreads) void tailbite_fused_kernel(
 // the sequence stays capturable in a HIP graph).
 __global__ void reset_counter_kernel(int32_t* counter) { *counter = 0; }
 
+
 // ------------------------------------------------- decode / pack / unpack
 // tensor_core_perm (quantize.py:101-118): element t -> row-major 16x16 index.
 __device__ __forceinline__ int tc_perm(int t) {

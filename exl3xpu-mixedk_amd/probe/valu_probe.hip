@@ -1,4 +1,6 @@
-// valu_probe.hip -- VALU issue-rate measurement for the forward DP's roofline.
+// valu_probe.hip -- VALU issue-rate measurement for the forward DP's roofline
+// (libxtqprobe.so, a benchmark helper: not part of the encoder library or
+// its C-ABI; bound by probe/valu_probe.py).
 //
 // The forward DP spends four instructions per trellis candidate: the
 // subtraction (v_add_f32 of -x with the codebook held in fp32 registers, or
@@ -17,7 +19,6 @@
 
 #include <stdint.h>
 
-#include "../../include/exl3_vit.h"
 
 namespace {
 
@@ -137,7 +138,14 @@ hipError_t launch_any(int which, int nwg, float* out, hipStream_t s) {
 
 }  // namespace
 
-extern "C" int xtq_valu_probe(int which, double* lane_ops_per_s) {
+// Times probe `which` (0 v_mul_f32, 1 v_add_f32, 2 v_fma_f32, 3 v_fma_mix_f32,
+// 4 v_min_f64, 5/6 the candidate mix with a packed fp16 codebook in
+// dependency order / grouped by opcode, 7/8 the mix with an fp32 codebook in
+// dependency order / grouped by opcode) on every CU of the current device
+// and returns its VALU lane-instructions per second.  Status: 0 ok, 1 no
+// device, 2 allocation failed, 4 HIP error, 8 unknown probe, 12 null output.
+extern "C" __attribute__((visibility("default"))) int xtq_valu_probe(int which,
+                                                                     double* lane_ops_per_s) {
     if (!lane_ops_per_s) return 12;
     if (which < 0 || which > 8) return 8;
     int dev = 0, ncu = 0;

@@ -1,31 +1,38 @@
 #!/usr/bin/env python3
-"""export_exl3.py -- write trellis-quantized tensors into an EXL3 model
-directory (the writer of the reference, quantize/export_exl3.py).
+"""export_exl3.py -- put trellis-quantized tensors into an EXL3 model directory.
 
-Inputs (--tensors ROOT) follow the reference's per-tensor layout
-(export_exl3.py:3-8):
+Drop-in for the reference's writer (quantize/export_exl3.py): the same
+functions, command line, input layout and exceptions.
+
+Input layout (--tensors ROOT), one file per quantized module:
 
     ROOT/L{nn}/{module}.safetensors   trellis int16 [k/16, n/16, 16K],
                                       suh fp16 [k], svh fp16 [n]
-    ROOT/L{nn}/{module}.json          optional metadata; "module" overrides
-                                      the file stem, other fields ("K",
-                                      "Wscale", ...) are informational
+    ROOT/L{nn}/{module}.json          optional metadata; its "module" names the
+                                      module when the file stem does not
 
-and map to the template keys model.language_model.layers.{nn}.{module}.{field}.
-The template (--template) is an EXL3 model directory (index + shards).  The
-output (--out) is the template with every provided tensor's bytes replaced in
-place inside its shard -- headers untouched, so writing the template's own
-tensors back gives byte-identical shards -- all other files copied verbatim
-and ARTIFACTS.sha256 rebuilt over the output files.
+A module's tensors land on model.language_model.layers.{nn}.{module}.{field}
+of the template (--template, an EXL3 model directory: index + shards).
 
-Checks (export_exl3.py:150-245): --selftest-a rebuilds the template from its
-own tensors and compares the shard bytes; --selftest-b decodes written
-tensors (HIP decode, then the inverse incoherence transform) and compares
-them with a saved W_hat; --check-keys verifies that every template key is in
-the output with its dtype and shape.
+How the output (--out) is made: every input is validated against the
+template's shard headers first (key present, dtype, shape, byte size); only
+then is anything written.  Shards are copied with the provided tensors'
+bytes overwritten where the template stores them, so headers never change
+and writing a template's own tensors back reproduces its shards byte for
+byte.  Other files are copied as they are and ARTIFACTS.sha256 is rebuilt
+over the output.
 
-write_quantized() is the harness side: it stores one quantize_linear result
-in the input layout.
+Checks: --selftest-a extracts the template's own decoder-layer tensors into
+the input layout and rebuilds the template from them (shards must be
+byte-identical); --selftest-b reconstructs written tensors with a decoder
+independent of the GPU kernels (torch integer ops on the bit stream, then
+the inverse incoherence transform) and compares them with a saved W_hat;
+--check-keys lists template keys missing from the output or stored there
+with another dtype or shape.
+
+write_quantized() is the quantizer side: it stores one quantize_linear
+result in the input layout.  weight_orig() is the GPU reconstruction (HIP
+decode) the quantizer itself uses.
 """
 from __future__ import annotations
 
@@ -39,66 +46,105 @@ import sys
 import tempfile
 from pathlib import Path
 
-# bytes per element of the safetensors dtypes
-ST_DTYPES = {"F64": 8, "F32": 4, "F16": 2, "BF16": 2, "I64": 8, "I32": 4,
-             "I16": 2, "I8": 1, "U8": 1, "BOOL": 1}
 QUANT_FIELDS = ("trellis", "suh", "svh")
 LAYER_PREFIX = "model.language_model.layers."
+INDEX_NAME = "model.safetensors.index.json"
+ARTIFACTS = "ARTIFACTS.sha256"
 
-_NUMPY_TO_ST = {"int16": "I16", "float16": "F16", "float32": "F32", "int32": "I32",
-                "int64": "I64", "uint8": "U8", "bool": "BOOL"}
-_ST_TO_TORCH = {"F16": "float16", "I16": "int16", "F32": "float32", "I32": "int32",
-                "BF16": "bfloat16", "I64": "int64", "U8": "uint8", "BOOL": "bool"}
+# safetensors dtype tag -> torch dtype name, for the tags an input may carry
+_TAG_TO_TORCH = {"I16": "int16", "F16": "float16", "F32": "float32", "I32": "int32",
+                 "I64": "int64", "U8": "uint8", "BOOL": "bool", "BF16": "bfloat16"}
+_INPUT_TAGS = frozenset(("I16", "F16", "F32", "I32", "I64", "U8", "BOOL"))
 
 
 # ------------------------------------------------------------ safetensors
+class _StFile:
+    """A safetensors file's header: tensor name -> (dtype tag, shape, absolute
+    first byte, absolute end byte).  The format is an 8-byte little-endian
+    header length, a JSON header with per-tensor data_offsets relative to the
+    data section, then the data section."""
+
+    def __init__(self, path):
+        self.path = Path(path)
+        with open(self.path, "rb") as f:
+            (hlen,) = struct.unpack("<Q", f.read(8))
+            self.header = json.loads(f.read(hlen))
+        self.data_start = 8 + hlen
+        self.entries = {}
+        for name, ent in self.header.items():
+            if name == "__metadata__":
+                continue
+            lo, hi = ent["data_offsets"]
+            self.entries[name] = (ent["dtype"], list(ent["shape"]), self.data_start + lo,
+                                  self.data_start + hi)
+
+    def read(self, name: str) -> bytes:
+        _, _, a, b = self.entries[name]
+        with open(self.path, "rb") as f:
+            f.seek(a)
+            return f.read(b - a)
+
+    def tensor(self, name: str):
+        """The tensor as a torch tensor (CPU, a copy)."""
+        import torch
+        tag, shape, _, _ = self.entries[name]
+        dtype = getattr(torch, _TAG_TO_TORCH[tag])
+        return torch.frombuffer(bytearray(self.read(name)), dtype=dtype).reshape(shape).clone()
+
+
 def read_st_header(path):
-    """(header dict, byte offset of the data section) of a safetensors file:
-    an 8-byte little-endian header length, the JSON header, then the data."""
-    with open(path, "rb") as f:
-        (hlen,) = struct.unpack("<Q", f.read(8))
-        header = json.loads(f.read(hlen))
-    return header, 8 + hlen
+    """(header dict, byte offset of the data section) of a safetensors file."""
+    f = _StFile(path)
+    return f.header, f.data_start
 
 
 def tensor_bytes(path, key):
     """Raw bytes of tensor `key` inside safetensors file `path`."""
-    header, base = read_st_header(path)
-    lo, hi = header[key]["data_offsets"]
-    with open(path, "rb") as f:
-        f.seek(base + lo)
-        return f.read(hi - lo)
+    return _StFile(path).read(key)
 
 
-def _layer_key(nn, module, field):
-    return f"{LAYER_PREFIX}{int(nn)}.{module}.{field}"
+def _weight_map(model_dir) -> dict:
+    return json.loads((Path(model_dir) / INDEX_NAME).read_text())["weight_map"]
+
+
+def _split_layer_key(key: str):
+    """'model.language_model.layers.{nn}.{module}.{field}' -> (nn, module,
+    field), or None for keys outside the decoder layers."""
+    if not key.startswith(LAYER_PREFIX):
+        return None
+    nn, _, rest = key[len(LAYER_PREFIX):].partition(".")
+    module, _, field = rest.rpartition(".")
+    return int(nn), module, field
 
 
 # ------------------------------------------------------------------ inputs
+def _input_files(tensors_root):
+    """(layer, module, path) of every input file, in path order."""
+    for path in sorted(Path(tensors_root).glob("L*/*.safetensors")):
+        module = path.stem
+        meta = path.with_suffix(".json")
+        if meta.exists():
+            module = json.loads(meta.read_text()).get("module", module)
+        yield int(path.parent.name[1:]), module, path
+
+
 def collect_inputs(tensors_root):
-    """Every quantized tensor under ROOT/L*/ -> {template key: (st dtype,
-    shape, raw bytes)}.  A file missing one of trellis/suh/svh raises
-    KeyError; an unsupported dtype raises ValueError."""
-    from safetensors import safe_open
+    """Every quantized tensor under ROOT/L*/ -> {template key: (dtype tag,
+    shape, raw bytes)}.  A file without one of trellis/suh/svh raises
+    KeyError; a dtype the template cannot hold raises ValueError."""
     found = {}
-    for st_path in sorted(Path(tensors_root).glob("L*/*.safetensors")):
-        nn = int(st_path.parent.name[1:])
-        module = st_path.stem
-        meta_path = st_path.with_suffix(".json")
-        if meta_path.exists():
-            module = json.loads(meta_path.read_text()).get("module", module)
-        with safe_open(str(st_path), framework="np") as f:
-            keys = set(f.keys())
-            missing = [fld for fld in QUANT_FIELDS if fld not in keys]
-            if missing:
-                raise KeyError(f"{st_path}: missing key {missing[0]!r} (has {sorted(keys)})")
-            for fld in QUANT_FIELDS:
-                arr = f.get_tensor(fld)
-                st_dtype = _NUMPY_TO_ST.get(str(arr.dtype))
-                if st_dtype is None:
-                    raise ValueError(f"{st_path}:{fld} dtype {arr.dtype}")
-                found[_layer_key(nn, module, fld)] = (st_dtype, list(arr.shape),
-                                                      arr.tobytes(order="C"))
+    for layer, module, path in _input_files(tensors_root):
+        st = _StFile(path)
+        for field in QUANT_FIELDS:
+            if field not in st.entries:
+                raise KeyError(f"{path}: no {field!r} tensor (it holds "
+                               f"{sorted(st.entries)})")
+        for field in QUANT_FIELDS:
+            tag, shape, _, _ = st.entries[field]
+            if tag not in _INPUT_TAGS:
+                raise ValueError(f"{path}:{field} has dtype {tag}, which the writer "
+                                 "does not take")
+            found[f"{LAYER_PREFIX}{layer}.{module}.{field}"] = (tag, shape, st.read(field))
     return found
 
 
@@ -107,243 +153,284 @@ def write_quantized(root, layer: int, module: str, result: dict, extra_meta=None
     ROOT/L{layer:02d}/{module}.safetensors plus its .json metadata."""
     import torch
     from safetensors.torch import save_file
-    ldir = Path(root) / f"L{int(layer):02d}"
-    ldir.mkdir(parents=True, exist_ok=True)
-    path = ldir / f"{module}.safetensors"
-    tensors = {"trellis": result["trellis"].to("cpu", torch.int16).contiguous(),
-               "suh": result["suh"].to("cpu", torch.float16).contiguous(),
-               "svh": result["svh"].to("cpu", torch.float16).contiguous()}
-    save_file(tensors, str(path))
-    meta = {"module": module, "K": int(result.get("K", tensors["trellis"].shape[-1] // 16))}
-    for k in ("Wscale", "code", "channel_scales", "use_ldlq"):
-        if k in result:
-            meta[k] = result[k]
+    path = Path(root) / f"L{int(layer):02d}" / f"{module}.safetensors"
+    path.parent.mkdir(parents=True, exist_ok=True)
+    want = {"trellis": torch.int16, "suh": torch.float16, "svh": torch.float16}
+    save_file({f: result[f].to("cpu", dt).contiguous() for f, dt in want.items()}, str(path))
+    meta = {"module": module, "K": int(result.get("K", result["trellis"].shape[-1] // 16))}
+    meta.update({k: result[k] for k in ("Wscale", "code", "channel_scales", "use_ldlq")
+                 if k in result})
     meta.update(extra_meta or {})
     path.with_suffix(".json").write_text(json.dumps(meta))
     return path
 
 
 # ------------------------------------------------------------------ export
-def _sha256(path):
+def _plan(inputs: dict, template: Path, weight_map: dict) -> dict:
+    """Validate every input against the template before any write: shard
+    name -> [(absolute offset, raw bytes, key)]."""
+    by_shard: dict = {}
+    for key in sorted(inputs):
+        shard = weight_map.get(key)
+        if shard is None:
+            raise KeyError(f"input key {key} is not in the template's index")
+        by_shard.setdefault(shard, []).append(key)
+    plan = {}
+    for shard, keys in by_shard.items():
+        st = _StFile(template / shard)
+        writes = []
+        for key in keys:
+            tag, shape, raw = inputs[key]
+            if key not in st.entries:
+                raise KeyError(f"input key {key} is not in template shard {shard}")
+            t_tag, t_shape, a, b = st.entries[key]
+            if tag != t_tag:
+                raise ValueError(f"{key}: dtype {tag} where the template has {t_tag}")
+            if shape != t_shape:
+                raise ValueError(f"{key}: shape {shape} where the template has {t_shape}")
+            if len(raw) != b - a:
+                raise ValueError(f"{key}: {len(raw)} bytes where the template has {b - a}")
+            writes.append((a, raw, key))
+        plan[shard] = writes
+    return plan
+
+
+def _sha256_file(path: Path) -> str:
     h = hashlib.sha256()
     with open(path, "rb") as f:
-        while True:
-            chunk = f.read(1 << 24)
-            if not chunk:
-                break
-            h.update(chunk)
+        for block in iter(lambda: f.read(1 << 24), b""):
+            h.update(block)
     return h.hexdigest()
+
+
+def _write_artifacts(outdir: Path):
+    """ARTIFACTS.sha256 over the output files, in sha256sum's format."""
+    names = sorted(p.name for p in outdir.iterdir() if p.is_file() and p.name != ARTIFACTS)
+    (outdir / ARTIFACTS).write_text(
+        "".join(f"{_sha256_file(outdir / n)}  {n}\n" for n in names))
 
 
 def export(tensors_root, template, outdir):
     """Splice the quantized tensors under tensors_root into a copy of the
-    template directory; returns the number of tensors replaced."""
+    template directory; returns the number of tensors written."""
     template, outdir = Path(template), Path(outdir)
-    weight_map = json.loads((template / "model.safetensors.index.json").read_text())["weight_map"]
+    weight_map = _weight_map(template)
     inputs = collect_inputs(tensors_root)
-    unknown = [k for k in inputs if k not in weight_map]
-    if unknown:
-        raise KeyError(f"input key {unknown[0]} not in template index")
-
-    by_shard: dict = {}
-    for key, blob in inputs.items():
-        by_shard.setdefault(weight_map[key], {})[key] = blob
-
+    plan = _plan(inputs, template, weight_map)
+    shards = set(weight_map.values())
     outdir.mkdir(parents=True, exist_ok=True)
-    shards = sorted(set(weight_map.values()))
-    written = set()
-    for shard in shards:
-        header, base = read_st_header(template / shard)
-        repl = by_shard.get(shard, {})
-        # validate everything for this shard before writing any byte of it
-        for key, (dt, shape, raw) in repl.items():
-            ent = header[key]
-            if ent["dtype"] != dt:
-                raise ValueError(f"{key}: dtype {dt} != template {ent['dtype']}")
-            if ent["shape"] != shape:
-                raise ValueError(f"{key}: shape {shape} != template {ent['shape']}")
-            lo, hi = ent["data_offsets"]
-            if hi - lo != len(raw):
-                raise ValueError(f"{key}: nbytes mismatch")
+    written = 0
+    for shard in sorted(shards):
         shutil.copyfile(template / shard, outdir / shard)
-        if repl:
+        writes = plan.get(shard, ())
+        if writes:
             with open(outdir / shard, "r+b") as f:
-                for key, (_, _, raw) in repl.items():
-                    f.seek(base + header[key]["data_offsets"][0])
+                for offset, raw, _ in writes:
+                    f.seek(offset)
                     f.write(raw)
-                    written.add(key)
-    if written != set(inputs):
-        raise RuntimeError(f"keys not written: {sorted(set(inputs) - written)}")
-
-    # configs, tokenizer, index, licence ...: verbatim
-    shard_set = set(shards)
+            written += len(writes)
+    if written != len(inputs):
+        raise RuntimeError(f"{len(inputs) - written} input tensors were not written")
     for item in template.iterdir():
-        if item.is_file() and item.name not in shard_set and item.name != "ARTIFACTS.sha256":
+        if item.is_file() and item.name not in shards and item.name != ARTIFACTS:
             shutil.copyfile(item, outdir / item.name)
-
-    lines = [f"{_sha256(item)}  {item.name}" for item in sorted(outdir.iterdir())
-             if item.is_file() and item.name != "ARTIFACTS.sha256"]
-    (outdir / "ARTIFACTS.sha256").write_text("\n".join(lines) + "\n")
-    return len(written)
+    _write_artifacts(outdir)
+    return written
 
 
 # ------------------------------------------------------------------ checks
 def selftest_a(template, workdir, only_keys=None):
-    """Extract the template's own decoder-layer quantized tensors into the
-    input layout under workdir/tensors; returns (root, files written).
-    Keys outside model.language_model.layers.* (lm_head, mtp.*) have no input
-    layout and keep the template bytes."""
-    import torch
+    """The template's own decoder-layer quantized tensors in the input layout
+    under workdir/tensors; returns (root, files written).  Keys outside
+    model.language_model.layers.* (lm_head, mtp.*) have no input layout and
+    keep the template bytes."""
     from safetensors.torch import save_file
     template = Path(template)
-    weight_map = json.loads((template / "model.safetensors.index.json").read_text())["weight_map"]
+    modules: dict = {}
+    shard_keys: dict = {}
+    for key, shard in _weight_map(template).items():
+        parts = _split_layer_key(key)
+        if parts is None or parts[2] not in QUANT_FIELDS:
+            continue
+        if only_keys is None or key in only_keys:
+            shard_keys.setdefault(shard, []).append((key, parts))
+    for shard, items in shard_keys.items():
+        st = _StFile(template / shard)
+        for key, (layer, module, field) in items:
+            modules.setdefault((layer, module), {})[field] = st.tensor(key)
     root = Path(workdir) / "tensors"
-    files: dict = {}
-    for key, shard in weight_map.items():
-        if not key.endswith(QUANT_FIELDS) or not key.startswith(LAYER_PREFIX):
-            continue
-        if only_keys is not None and key not in only_keys:
-            continue
-        parts = key[len(LAYER_PREFIX):].split(".")
-        nn, module, field = parts[0], ".".join(parts[1:-1]), parts[-1]
-        header, _ = read_st_header(template / shard)
-        ent = header[key]
-        dtype = getattr(torch, _ST_TO_TORCH[ent["dtype"]])
-        raw = bytearray(tensor_bytes(template / shard, key))
-        t = torch.frombuffer(raw, dtype=dtype).reshape(ent["shape"]).clone()
-        path = root / f"L{nn}" / f"{module}.safetensors"
-        files.setdefault(path, {})[field] = t
-    for path, tensors in files.items():
+    for (layer, module), tensors in sorted(modules.items()):
+        path = root / f"L{layer}" / f"{module}.safetensors"
         path.parent.mkdir(parents=True, exist_ok=True)
         save_file(tensors, str(path))
         K = int(tensors["trellis"].shape[-1]) // 16 if "trellis" in tensors else 4
-        path.with_suffix(".json").write_text(json.dumps({"module": path.stem, "K": K}))
-    return root, len(files)
+        path.with_suffix(".json").write_text(json.dumps({"module": module, "K": K}))
+    return root, len(modules)
 
 
 def weight_orig(trellis, suh, svh, K: int, code: str = "exl3_mul1", device=None):
     """Original-basis weight [k, n] fp32 of one EXL3 tensor: the HIP trellis
-    decode followed by diag(suh) B W_inner B diag(svh) (the inverse
-    incoherence transform, quantize.py:158-164).  quantize_linear builds its
-    W_hat with the same operations, so W_hat == weight_orig(...).t() when
-    both run on the same device."""
+    decode, then diag(suh) B W_inner B diag(svh) (the inverse incoherence
+    transform, quantize.py:158-164).  quantize_linear builds W_hat with the
+    same operations, so W_hat == weight_orig(...).t() on the same device."""
     import torch
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     import hip_backend as hb
     import quantize as xq
     dev = torch.device(device) if device is not None else torch.device("cuda")
-    tr = trellis.to("cuda", torch.int16).contiguous()
-    w_inner = hb.decode(tr, int(K), code=hb.code_name(code)).to(dev)
-    h = xq.hadamard128(dev, torch.float32)
-    return xq.from_inner(w_inner, suh.to(dev), svh.to(dev), h)
+    w_inner = hb.decode(trellis.to("cuda", torch.int16).contiguous(), int(K),
+                        code=hb.code_name(code)).to(dev)
+    return xq.from_inner(w_inner, suh.to(dev), svh.to(dev), xq.hadamard128(dev, torch.float32))
+
+
+def _states_from_stream(trellis, K: int):
+    """int16 [tiles, 16K] -> int64 states [tiles, 256] with torch integer ops
+    (no GPU kernel): the stream's 32-bit words are (lo16 | hi16 << 16), bit b
+    of the stream is bit 31 - b%32 of word b/32, and s_t is the 16 stream
+    bits ending at bit (t+1)K - 1, read circularly, MSB first
+    (quantize.py:381-402)."""
+    import torch
+    t16 = trellis.to(torch.int64) & 0xFFFF
+    words = t16[:, 0::2] | (t16[:, 1::2] << 16)                   # [tiles, 8K]
+    nbits = 256 * K
+    b = torch.arange(nbits, device=trellis.device)
+    bits = (words[:, b // 32] >> (31 - b % 32)) & 1                 # [tiles, 256K]
+    t = torch.arange(256, device=trellis.device).unsqueeze(1)
+    k = torch.arange(16, device=trellis.device).unsqueeze(0)
+    idx = (t * K + K - 16 + k) % nbits                              # [256, 16]
+    weights = (1 << (15 - torch.arange(16, device=trellis.device)))
+    return (bits[:, idx] * weights).sum(dim=2)
+
+
+def weight_orig_torch(trellis, suh, svh, K: int, code: str = "exl3_mul1", device=None,
+                      tiles_per_block: int = 4096):
+    """weight_orig through a decoder independent of the GPU kernels: the bit
+    stream is unpacked with torch integer ops (_states_from_stream), mapped
+    through the codebook table and placed by the tensor-core permutation
+    (quantize.py:101-118,405-415), then taken through the same inverse
+    incoherence transform.  The check --selftest-b runs."""
+    import torch
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import quantize as xq
+    dev = torch.device(device) if device is not None else torch.device("cuda")
+    tk, tn, w = trellis.shape
+    if w != 16 * K:
+        raise ValueError(f"trellis last dim {w} != 16 K = {16 * K}")
+    lut = xq.get_lut(code).to(dev, torch.float32)
+    perm = xq.tensor_core_perm().to(dev)
+    flat = trellis.to(dev).reshape(tk * tn, w)
+    tiles = torch.empty(tk * tn, 256, dtype=torch.float32, device=dev)
+    for a in range(0, tk * tn, tiles_per_block):
+        st = _states_from_stream(flat[a:a + tiles_per_block], K)
+        tiles[a:a + tiles_per_block, perm] = lut[st]
+    w_inner = tiles.view(tk, tn, 16, 16).permute(0, 2, 1, 3).reshape(16 * tk, 16 * tn)
+    return xq.from_inner(w_inner, suh.to(dev), svh.to(dev), xq.hadamard128(dev, torch.float32))
+
+
+def _module_fields(model_dir: Path, weight_map: dict, base: str) -> dict:
+    """trellis/suh/svh of one module, wherever the index puts each field."""
+    return {f: _StFile(model_dir / weight_map[f"{base}.{f}"]).tensor(f"{base}.{f}")
+            for f in QUANT_FIELDS}
 
 
 def selftest_b(template, outdir, what_if, device=None):
-    """For each "L{nn}/{module}|W_hat.pt" spec: weight_orig of the written
-    tensor == the saved W_hat [out, in].  Returns [(spec, equal, maxabs)]."""
+    """For each "L{nn}/{module}|W_hat.pt" spec: the written tensor,
+    reconstructed by weight_orig_torch (a decoder independent of the
+    quantizer's), equals the saved W_hat [out, in].  Returns
+    [(spec tensor, equal, max abs difference)]."""
     import torch
-    from safetensors import safe_open
-    weight_map = json.loads(
-        (Path(outdir) / "model.safetensors.index.json").read_text())["weight_map"]
+    outdir = Path(outdir)
+    weight_map = _weight_map(outdir)
     results = []
     for spec in what_if:
         tensor_ref, w_path = spec.split("|")
         ldir, module = tensor_ref.split("/", 1)
-        base = f"{LAYER_PREFIX}{int(ldir[1:])}.{module}"
-        fields = {}
-        for fld in QUANT_FIELDS:            # a module's fields may sit in different shards
-            with safe_open(str(Path(outdir) / weight_map[f"{base}.{fld}"]), framework="pt") as f:
-                fields[fld] = f.get_tensor(f"{base}.{fld}")
-        trellis, suh, svh = fields["trellis"], fields["suh"], fields["svh"]
-        K = int(trellis.shape[-1]) // 16
-        w = weight_orig(trellis, suh, svh, K, device=device).t().contiguous().cpu()
-        W_hat = torch.load(w_path, map_location="cpu", weights_only=True)
-        results.append((tensor_ref, bool(torch.equal(w, W_hat.contiguous())),
+        fields = _module_fields(outdir, weight_map, f"{LAYER_PREFIX}{int(ldir[1:])}.{module}")
+        K = int(fields["trellis"].shape[-1]) // 16
+        w = weight_orig_torch(fields["trellis"], fields["suh"], fields["svh"], K,
+                              device=device).t().contiguous().cpu()
+        W_hat = torch.load(w_path, map_location="cpu", weights_only=True).contiguous()
+        results.append((tensor_ref, bool(torch.equal(w, W_hat)),
                         float((w - W_hat).abs().max())))
     return results
 
 
 def check_keys(template, outdir):
-    """[(key, problem)] for template keys missing from the output or with a
-    different dtype/shape there."""
+    """[(key, problem)] for template keys missing from the output's index or
+    shard, or stored there with another dtype or shape."""
     template, outdir = Path(template), Path(outdir)
-    t_map = json.loads((template / "model.safetensors.index.json").read_text())["weight_map"]
-    o_map = json.loads((outdir / "model.safetensors.index.json").read_text())["weight_map"]
-    headers: dict = {}
+    t_map, o_map = _weight_map(template), _weight_map(outdir)
+    opened: dict = {}
 
-    def header(path):
-        if path not in headers:
-            headers[path] = read_st_header(path)[0]
-        return headers[path]
+    def entries(path: Path):
+        if path not in opened:
+            opened[path] = _StFile(path).entries
+        return opened[path]
 
     problems = []
     for key, shard in t_map.items():
         if key not in o_map:
             problems.append((key, "missing-from-index"))
             continue
-        te = header(template / shard).get(key)
-        oe = header(outdir / o_map[key]).get(key)
-        if oe is None:
+        o_ent = entries(outdir / o_map[key]).get(key)
+        if o_ent is None:
             problems.append((key, "missing-in-shard"))
-        elif (te["dtype"], te["shape"]) != (oe["dtype"], oe["shape"]):
-            problems.append((key, f"{te['dtype']}{te['shape']} vs {oe['dtype']}{oe['shape']}"))
+            continue
+        t_tag, t_shape = entries(template / shard)[key][:2]
+        if (t_tag, t_shape) != o_ent[:2]:
+            problems.append((key, f"{t_tag}{t_shape} vs {o_ent[0]}{o_ent[1]}"))
     return problems
 
 
-def _same_bytes(a: Path, b: Path) -> bool:
-    if a.stat().st_size != b.stat().st_size:
-        return False
-    with open(a, "rb") as fa, open(b, "rb") as fb:
-        while True:
-            x, y = fa.read(1 << 24), fb.read(1 << 24)
-            if x != y:
-                return False
-            if not x:
-                return True
+def _files_equal(a: Path, b: Path) -> bool:
+    return a.stat().st_size == b.stat().st_size and _sha256_file(a) == _sha256_file(b)
 
 
 def main(argv=None):
-    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    ap.add_argument("--tensors")
-    ap.add_argument("--template", required=True)
-    ap.add_argument("--out", required=True)
+    ap = argparse.ArgumentParser(description="Write trellis-quantized tensors into an EXL3 "
+                                             "model directory.")
+    ap.add_argument("--tensors", help="input root: L{nn}/{module}.safetensors (+ .json)")
+    ap.add_argument("--template", required=True, help="EXL3 model directory to start from")
+    ap.add_argument("--out", required=True, help="output model directory")
     ap.add_argument("--selftest-a", action="store_true",
-                    help="rebuild the template from its own tensors; the output shards "
-                         "must be byte-identical")
+                    help="rebuild the template from its own tensors and require "
+                         "byte-identical shards")
     ap.add_argument("--selftest-b", nargs="*", default=None, metavar="L{nn}/{module}|W_hat.pt",
-                    help="weight_orig(written tensor) == saved W_hat for each spec")
-    ap.add_argument("--check-keys", action="store_true")
+                    help="reconstruct each written tensor independently and require it "
+                         "to equal the saved W_hat")
+    ap.add_argument("--check-keys", action="store_true",
+                    help="list template keys missing from the output or changed in "
+                         "dtype/shape")
     ap.add_argument("--tmpdir", default=None,
-                    help="scratch dir for --selftest-a (default: XTQ_TMPDIR or the parent "
-                         "of --out)")
+                    help="where --selftest-a extracts (default: XTQ_TMPDIR, else the "
+                         "directory holding --out)")
     args = ap.parse_args(argv)
 
     if args.selftest_a:
-        parent = args.tmpdir or os.environ.get("XTQ_TMPDIR") or str(Path(args.out).parent)
-        Path(parent).mkdir(parents=True, exist_ok=True)
-        with tempfile.TemporaryDirectory(dir=parent) as td:
+        scratch = Path(args.tmpdir or os.environ.get("XTQ_TMPDIR") or Path(args.out).parent)
+        scratch.mkdir(parents=True, exist_ok=True)
+        with tempfile.TemporaryDirectory(dir=scratch) as td:
             root, n = selftest_a(args.template, td)
-            print(f"selftest-a: extracted {n} module(s) -> {root}")
+            print(f"selftest-a: {n} module(s) extracted to {root}")
             export(root, args.template, args.out)
-            same = True
-            for shard in sorted(Path(args.out).glob("*.safetensors")):
-                if not _same_bytes(shard, Path(args.template) / shard.name):
-                    print(f"  DIFFERS: {shard.name}")
-                    same = False
-            print(f"selftest-a: shards byte-identical: {same}")
-            return 0 if same else 1
+            differ = [p.name for p in sorted(Path(args.out).glob("*.safetensors"))
+                      if not _files_equal(p, Path(args.template) / p.name)]
+            for name in differ:
+                print(f"  DIFFERS: {name}")
+            print(f"selftest-a: shards byte-identical: {not differ}")
+            return 1 if differ else 0
     if not args.tensors:
-        ap.error("--tensors is required unless --selftest-a")
+        ap.error("--tensors is required unless --selftest-a is given")
     n = export(args.tensors, args.template, args.out)
-    print(f"export: replaced {n} tensors -> {args.out}")
+    print(f"export: {n} tensors written to {args.out}")
     rc = 0
     if args.selftest_b:
         for ref, eq, mx in selftest_b(args.template, args.out, args.selftest_b):
-            print(f"selftest-b {ref}: equal={eq} maxabs={mx:.3e}")
+            print(f"selftest-b {ref}: equal={eq} max|diff|={mx:.3e}")
             rc |= 0 if eq else 1
     if args.check_keys:
         bad = check_keys(args.template, args.out)
-        print(f"check-keys: {len(bad)} problems")
+        print(f"check-keys: {len(bad)} problem(s)")
         for b in bad[:20]:
             print("  ", b)
         rc |= 1 if bad else 0

@@ -68,8 +68,6 @@ def lib():
         lp = ctypes.POINTER(ctypes.c_int64)
         L.xtq_vit_prof_read.argtypes = [dp, lp, dp, dp, lp]
         L.xtq_vit_prof_read.restype = i32
-        L.xtq_valu_probe.argtypes = [i32, dp]
-        L.xtq_valu_probe.restype = i32
         L.xtq_vit_strerror.argtypes = [i32]
         L.xtq_vit_strerror.restype = cp
         for fn in ("xtq_vit_init", "xtq_vit_run", "xtq_vit_run_k", "xtq_vit_tailbite_dev",
@@ -287,20 +285,6 @@ def scratch_per_seq(K: int) -> int:
 def prof_enable(on: bool = True):
     """Bracket every forward/traceback launch with HIP events (benchmarks)."""
     lib().xtq_vit_prof_enable(1 if on else 0)
-
-
-VALU_PROBES = ("v_mul_f32", "v_add_f32", "v_fma_f32", "v_fma_mix_f32", "v_min_f64",
-               "candidate mix, dependency order", "candidate mix, grouped by opcode",
-               "fp32-code candidate mix, dependency order",
-               "fp32-code candidate mix, grouped by opcode")
-
-
-def valu_probe(which: int) -> float:
-    """VALU lane-instructions/s of probe `which` (VALU_PROBES) on the current
-    device (xtq_valu_probe)."""
-    v = ctypes.c_double()
-    _check("xtq_valu_probe", lib().xtq_valu_probe(int(which), ctypes.byref(v)))
-    return v.value
 
 
 def prof_read() -> dict:

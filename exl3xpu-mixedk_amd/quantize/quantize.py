@@ -421,8 +421,7 @@ def ldlq_viterbi(Wq: torch.Tensor, Lfac: torch.Tensor | None, lut: torch.Tensor,
         hatW, states, trellis, xt = _hb.ldlq_chain(
             Wg, Lg, K, piv, int(margin), code=kcode, states=True,
             targets=bool(ldlq_viterbi.keep_targets))
-        if progress is not None:
-            progress(0, 512 * tk)
+        _chain_progress(progress, tk)
         ldlq_viterbi.last_trellis = trellis
         ldlq_viterbi.last_targets = xt
         return hatW.to(dev), states.long().to(dev)
@@ -461,6 +460,17 @@ def ldlq_viterbi(Wq: torch.Tensor, Lfac: torch.Tensor | None, lut: torch.Tensor,
     _hb.status(gdev)                 # NaN targets anywhere in the sweep raise here
     ldlq_viterbi.last_trellis = trellis
     return hatW_t.t().contiguous(), states.long().to(dev)
+
+
+def _chain_progress(progress, tk: int):
+    """The reference's per-block progress sequence (quantize.py:666,732-734):
+    progress(i, 512 * blocks done) for the 16-row blocks i = tk-1 .. 0 in
+    sweep order.  The column-chain schedule encodes all blocks in one launch,
+    so the calls follow its completion."""
+    if progress is None:
+        return
+    for d, i in enumerate(range(tk - 1, -1, -1), start=1):
+        progress(i, 512 * d)
 
 
 ldlq_viterbi.last_trellis = None
@@ -632,8 +642,7 @@ def quantize_linear_group(Ws, H_x: torch.Tensor | None, code: str = "exl3_mul1",
         ldlq_viterbi.last_targets = xt
         ldlq_viterbi.last_trellis = None
         ldlq_viterbi.last_groups = [(r[0], r[1], r[2], t) for r, t in zip(runs, run_tr)]
-        if progress is not None:
-            progress(0, 512 * (Wq.shape[0] // 16))
+        _chain_progress(progress, Wq.shape[0] // 16)
     else:
         hatWq = torch.empty_like(Wq)
         states = torch.empty(Wq.shape[0] // 16, Wq.shape[1] // 16, 256, dtype=torch.long,

@@ -20,6 +20,10 @@ channels, rank min(n_s, d) before the quantizer's own 1 % damping
   c5  17408-in x 5120-out down projection, Student-t(5) scaled to std 0.02,
       AR(1) rho=0.5 at d=17408 from n_s=4096 samples, K=6 (and K=4)
 
+c5_tiles() gives the kernel-throughput workload: every 16x16 tile of c5's
+weight after the incoherence transform and the unit-rms scale, without
+BlockLDLQ feedback (348,160 independent 256-step sequences).
+
 Shapes are nn.Linear [out, in]; H is [in, in].  `scale` shrinks every
 dimension by an integer factor (multiples of 128 kept) for quick checks.
 """
@@ -106,3 +110,28 @@ def c5(scale: int = 1, device="cpu") -> dict:
     W = c5_weight(device, scale)
     H = ar1_gram(W.shape[1], _dim(4096, scale), 0.5, 4, device)
     return {"name": "c5", "W": W, "H": H, "Ks": (6, 4), "channel_scales": False}
+
+
+def c5_tiles(device="cuda", seed: int = 4) -> torch.Tensor:
+    """The 348,160 tile targets of c5's weight without feedback: random-sign
+    + Hadamard incoherence (signs from seeds 20261011 / 20261012, as
+    quantize_linear), the unit-rms scale against the mul1 codebook, and each
+    16x16 tile's sequence x_t = tile[perm[t]] -> [348160, 256] fp32 on
+    `device` (tile (a, b) of the [17408 in, 5120 out] inner weight at row
+    a * 320 + b)."""
+    import quantize as xq
+    dev = torch.device(device)
+    W = c5_weight(dev, seed=seed).float()                    # [5120 out, 17408 in]
+    out_f, in_f = W.shape
+    suh = xq.sign_vec(in_f, 20261011, dev).half()
+    svh = xq.sign_vec(out_f, 20261012, dev).half()
+    h = xq.hadamard128(dev, torch.float32)
+    Wi = xq.to_inner(W.t().contiguous(), suh, svh, h)         # [k, n]
+    del W
+    lut_rms = xq.get_lut("exl3_mul1").double().square().mean().sqrt().float()
+    Wq = Wi / (Wi.square().mean().sqrt() / lut_rms.to(dev))
+    del Wi
+    tk, tn = in_f // 16, out_f // 16
+    perm = xq.tensor_core_perm().to(dev)
+    X = Wq.view(tk, 16, tn, 16).permute(0, 2, 1, 3).reshape(tk * tn, 256)[:, perm]
+    return X.contiguous()

@@ -17,25 +17,35 @@
  *   - X is [nseq][256] fp32, C-contiguous, one sequence per tile in the
  *     sequence order x_t = tile[perm[t]] (quantize.py:684-686).
  *
- * Status codes:
+ * Status codes (1-6 keep the reference's numbers and meaning):
  *   0  ok
  *   1  initialisation failed (no HIP device, HIP error during init)
  *   2  device allocation failed
  *   3  XTQ_VIT_DEVIDX names no device
  *   4  HIP runtime error during a run
- *   5  request exceeds XTQ_VIT_MAXBYTES (device bytes for X/states/scratch)
- *   6  nseq <= 0 or nseq > XTQ_VIT_MAXSEQ
+ *   5  host-pointer entries: nseq * 1,317,888 B > XTQ_VIT_MAXBYTES (the
+ *      reference's check); any entry: library-owned device bytes would
+ *      exceed XTQ_VIT_DEV_MAXBYTES
+ *   6  nseq <= 0, or nseq > XTQ_VIT_MAXSEQ on the host-pointer entries;
+ *      bad shapes on the device entries
  *   8  unsupported code (e.g. "ih2x2"; only fp16-exact V=1 codebooks run)
  *   9  K outside 2..7 (or K != 4 for the K=4-only reference codes)
- *  10  pivot outside [0,256) or margin < 0
+ *  10  pivot outside [0,256), or margin < 0 on the entries the reference
+ *      has no counterpart for (xtq_vit_run treats margin < 0 as 0, as the
+ *      reference kernel does; the reference reads outside X for such a
+ *      pivot, its torch path asserts)
  *  11  a target is NaN
- *  12  null pointer argument
+ *  12  null or misaligned pointer argument
  *
- * Environment:
+ * Environment (read on every call):
  *   XTQ_VIT_DEVIDX   device index for the host-pointer entries (default: the
  *                    calling thread's current HIP device)
- *   XTQ_VIT_MAXSEQ   upper bound on nseq per call (default 1<<24)
- *   XTQ_VIT_MAXBYTES upper bound on library-owned device bytes (default 64 GiB)
+ *   XTQ_VIT_MAXSEQ   upper bound on nseq per host-pointer call (default
+ *                    4096, the reference's)
+ *   XTQ_VIT_MAXBYTES bound on nseq * 1,317,888 B per host-pointer call
+ *                    (default 6 GiB, the reference's accounting)
+ *   XTQ_VIT_DEV_MAXBYTES upper bound on library-owned device bytes (default
+ *                    64 GiB; no reference counterpart)
  *   XTQ_VIT_SCRATCH  backpointer scratch budget in bytes; larger batches are
  *                    processed in chunks (default 8 GiB)
  *   XTQ_VIT_GROUP    force 1, 2, 4 or 8 sequences per forward workgroup
@@ -77,6 +87,9 @@ XTQ_API int xtq_vit_init(void);
  *   code  "mul1p", "mul1" or "mul1t" (the reference's K=4 mul1 kernels; all
  *         three give identical results); "ih2x2" returns 8
  *   out   [nseq][256] int32 host: the pass-2 states
+ * Bounds as the reference's: nseq <= XTQ_VIT_MAXSEQ (default 4096, else 6),
+ * nseq * 1,317,888 <= XTQ_VIT_MAXBYTES (default 6 GiB, else 5); margin < 0
+ * runs pass 1 over the whole sequence, as margin 0.
  */
 XTQ_API int xtq_vit_run(const float* X, int nseq, const char* code, int margin, int pivot,
                 int32_t* out);
@@ -218,21 +231,6 @@ XTQ_API int64_t xtq_vit_scratch_per_seq(int K);
 XTQ_API int xtq_vit_prof_enable(int on);
 XTQ_API int xtq_vit_prof_read(double* fwd_ms, int64_t* fwd_launches, double* fwd_seq_steps,
                       double* tb_ms, int64_t* tb_launches);
-
-/*
- * VALU issue-rate probe (no reference counterpart; a measurement helper for
- * the forward DP's roofline).  Times one probe kernel on every CU of the
- * current device and returns its VALU lane-instructions per second:
- *   0 v_mul_f32, 1 v_add_f32, 2 v_fma_f32, 3 v_fma_mix_f32, 4 v_min_f64,
- *   5 the DP's candidate mix with the codebook as packed fp16 (v_fma_mix_f32,
- *     v_mul_f32, v_add_f32, v_min_f64) in dependency order, 6 the same mix
- *     grouped by opcode, 7 the mix with the codebook in fp32 (v_add_f32,
- *     v_mul_f32, v_add_f32, v_min_f64) in dependency order, 8 that mix
- *     grouped by opcode.
- * Returns 8 for an unknown probe, 2 if its small output buffer cannot be
- * allocated, 4 on a HIP error.
- */
-XTQ_API int xtq_valu_probe(int which, double* lane_ops_per_s);
 
 /* Static description of a status code. */
 XTQ_API const char* xtq_vit_strerror(int rc);

@@ -121,9 +121,10 @@ static void dp_step(int K, int L, const float *lut, const float *b, float xp,
  *            state at step back_from in states[0] (quantize.py:305-312).
  * Scratch is passed in so batch drivers can reuse it per thread.
  */
-static int viterbi_run(const float *x, int T, const float *lut, int K, int L,
-                       int overlap, int back_from, int32_t *states,
-                       float *cost, float *best, int32_t *bw, uint8_t *from_state)
+static __attribute__((noinline)) int
+viterbi_run(const float *x, int T, const float *lut, int K, int L, int overlap,
+            int back_from, int32_t *states, float *cost, float *best, int32_t *bw,
+            uint8_t *from_state)
 {
     const int S = 1 << L, SP = 1 << (L - K);
     const float INF = INFINITY;

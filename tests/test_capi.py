@@ -57,7 +57,8 @@ def test_status_codes_without_device(lib):
     assert lib.xtq_vit_run(None, 2, b"mul1p", 0, 128, sp) == 12
     assert lib.xtq_vit_run(xp, 0, b"mul1p", 0, 128, sp) == 6
     assert lib.xtq_vit_run(xp, 2, b"mul1p", 0, 256, sp) == 10
-    assert lib.xtq_vit_run(xp, 2, b"mul1p", -1, 0, sp) == 10
+    assert lib.xtq_vit_run(xp, 2, b"mul1p", 0, -1, sp) == 10
+    assert lib.xtq_vit_run_k(xp, 2, 4, b"mul1", -1, 0, sp) == 10
     assert lib.xtq_vit_run_k(xp, 2, 8, b"mul1", 0, 0, sp) == 9
     assert lib.xtq_vit_run_k(xp, 2, 1, b"mul1", 0, 0, sp) == 9
     fake = ctypes.c_void_p(16)          # never dereferenced: rejected first
@@ -94,12 +95,49 @@ def test_status_codes_without_device(lib):
     assert chm(fake, None, 64, 64, 9, i2(32, 32), i2(4, 7), *args, tp2, None, None) == 6
     assert chm(fake, None, 64, 64, 2, i2(32, 32), i2(4, 7), *args, tp1, None, None) == 12
     assert chm(fake, None, 64, 64, 2, None, i2(4, 7), *args, tp2, None, None) == 12
-    out = ctypes.c_double()
-    assert lib.xtq_valu_probe(9, ctypes.byref(out)) == 8
-    assert lib.xtq_valu_probe(-1, ctypes.byref(out)) == 8
-    assert lib.xtq_valu_probe(0, None) == 12
     assert lib.xtq_vit_strerror(11) == b"NaN target"
     assert lib.xtq_vit_strerror(99) == b"unknown status"
+
+
+def test_host_entry_bounds(lib, monkeypatch):
+    """xtq_vit_run keeps the reference's bounds and their order
+    (viterbi_esimd.cpp:924-933,973-982): nseq <= XTQ_VIT_MAXSEQ (default
+    4096) else 6, then nseq * 1,317,888 B <= XTQ_VIT_MAXBYTES (default 6 GiB)
+    else 5, both read on every call; all before any device work."""
+    for v in ("XTQ_VIT_MAXSEQ", "XTQ_VIT_MAXBYTES"):
+        monkeypatch.delenv(v, raising=False)
+    X = np.zeros((1, 256), np.float32)
+    st = np.zeros((1, 256), np.int32)
+    xp = X.ctypes.data_as(ctypes.c_void_p)
+    sp = st.ctypes.data_as(ctypes.c_void_p)
+    assert lib.xtq_vit_run(xp, 4097, b"mul1p", 0, 128, sp) == 6
+    assert lib.xtq_vit_run_k(xp, 4097, 4, b"mul1", 0, 128, sp) == 6
+    assert lib.xtq_vit_run(xp, -3, b"mul1p", 0, 128, sp) == 6
+    monkeypatch.setenv("XTQ_VIT_MAXSEQ", "100000")
+    # 5000 * 1,317,888 B = 6.14 GiB > 6 GiB
+    assert lib.xtq_vit_run(xp, 5000, b"mul1p", 0, 128, sp) == 5
+    monkeypatch.setenv("XTQ_VIT_MAXBYTES", str(1317888 * 3 - 1))
+    assert lib.xtq_vit_run(xp, 3, b"mul1p", 0, 128, sp) == 5
+    monkeypatch.setenv("XTQ_VIT_MAXSEQ", "2")
+    assert lib.xtq_vit_run(xp, 3, b"mul1p", 0, 128, sp) == 6      # 6 is checked first
+
+
+def test_probe_library_is_separate(lib):
+    """The VALU probe is a benchmark helper in its own library: the encoder
+    library exports no probe symbol, the probe library rejects bad input."""
+    out = subprocess.run(["nm", "-D", "--defined-only", os.path.join(PKG, "lib", "libexl3vit.so")],
+                         capture_output=True, text=True, check=True).stdout
+    assert "xtq_valu_probe" not in out
+    sys_path = os.path.join(PKG, "probe")
+    import sys
+    if sys_path not in sys.path:
+        sys.path.insert(0, sys_path)
+    import valu_probe
+    pl = valu_probe.lib()
+    v = ctypes.c_double()
+    assert pl.xtq_valu_probe(9, ctypes.byref(v)) == 8
+    assert pl.xtq_valu_probe(-1, ctypes.byref(v)) == 8
+    assert pl.xtq_valu_probe(0, None) == 12
 
 
 def test_scratch_sizes(lib):

@@ -106,7 +106,7 @@ def test_export_errors(template, tmp_path):
     # key not in the template
     root = tmp_path / "unknown"
     ex.write_quantized(root, 7, "self_attn.q_proj", _fake_result(256, 384, 5, 1))
-    with pytest.raises(KeyError, match="not in template"):
+    with pytest.raises(KeyError, match="not in the template"):
         ex.export(root, template, tmp_path / "o3")
     # missing field
     root = tmp_path / "missing"
@@ -125,3 +125,22 @@ def test_check_keys_reports_problems(template, tmp_path):
     del idx["weight_map"][gone]
     (out / "model.safetensors.index.json").write_text(json.dumps(idx))
     assert ex.check_keys(template, out) == [(gone, "missing-from-index")]
+
+
+@pytest.mark.parametrize("K", (2, 5, 7))
+def test_independent_decoder_vs_oracle(oracle_mod, K):
+    """The --selftest-b decoder (torch integer ops, no GPU kernel) unpacks
+    and decodes random trellis streams exactly as the oracle does
+    (quantize.py:381-415), and its weight is from_inner of that decode."""
+    import quantize as xq
+    g = torch.Generator().manual_seed(K)
+    tr = torch.randint(-32768, 32768, (8, 8, 16 * K), generator=g, dtype=torch.int16)
+    st = ex._states_from_stream(tr.view(-1, 16 * K), K)
+    assert torch.equal(st, torch.from_numpy(oracle_mod.unpack(tr.view(-1, 16 * K).numpy(), K))
+                       .long())
+    suh, svh = torch.randn(128, generator=g).half(), torch.randn(128, generator=g).half()
+    w = ex.weight_orig_torch(tr, suh, svh, K, device="cpu")
+    lut = oracle_mod.code_lut("exl3_mul1")
+    inner = torch.from_numpy(oracle_mod.decode(tr.numpy(), lut, K))
+    h = xq.hadamard128("cpu", torch.float32)
+    assert torch.equal(w, xq.from_inner(inner, suh, svh, h))

@@ -208,3 +208,100 @@ def test_block_ldl_device_large(xq):
     with pytest.raises(RuntimeError):
         xq.block_LDL(B + B.t(), 16)
     assert torch.backends.cuda.preferred_linalg_library() == before
+
+
+def test_quantize_with_U_on_device(xq, oracle_mod, mul1_lut, cpu8):
+    """quantize() with a U factor on device tensors (quantize.py:944-950): the
+    U -> L conversion (triangular solve, G = U^-1 U^-T, block LDL) runs on
+    the GPU in fp64 and agrees with the CPU conversion to fp64 rounding; the
+    sweep (column chains) encodes every tile bit-exactly for the targets the
+    kernel computed; the result matches the reference's golden output up to
+    the feedback rounding of the GPU (its fp32 sums are not the CPU GEMM's,
+    so a tile whose targets move by an ulp may encode differently)."""
+    e = load_golden("e2e_128.npz")
+    Wt = torch.from_numpy(e["prep_Wt"])
+    U = torch.from_numpy(e["q_U"])
+    eye = torch.eye(U.shape[0], dtype=torch.float64)
+    Lc = []
+    for dev in ("cpu", "cuda"):
+        Uu = U.double().to(dev)
+        Ui = torch.linalg.solve_triangular(Uu, eye.to(dev), upper=True)
+        Lc.append(xq.block_LDL(Ui @ Ui.t(), 16)[0].cpu())
+    rel = float((Lc[1] - Lc[0]).norm() / Lc[0].norm())
+    print(f"U->L on the GPU vs CPU: relative difference {rel:.2e}", flush=True)
+    assert rel < 1e-12
+    print("case quantize() with U on cuda, margin 16, seed 147", flush=True)
+    xq.ldlq_viterbi.keep_targets = True
+    try:
+        W_hat, packed, scale = xq.quantize(Wt.cuda(), U.cuda(), "exl3_mul1", 4, seed=147,
+                                           margin=16)
+        xt = xq.ldlq_viterbi.last_targets
+    finally:
+        xq.ldlq_viterbi.keep_targets = False
+        xq.ldlq_viterbi.last_targets = None
+    assert W_hat.is_cuda and packed.is_cuda
+    # the scale is a device mean here: its reduction order may move the last bit
+    assert abs(np.float32(scale) - e["q_scale"]) <= np.spacing(e["q_scale"])
+    st = oracle_mod.unpack(packed.cpu().numpy().reshape(-1, 64), 4)
+    want = oracle_mod.tailbite(xt.reshape(-1, 256).cpu().numpy(), mul1_lut, 4, 16, pivot=147,
+                               margin=16)
+    np.testing.assert_array_equal(st, want)
+    diff_tiles = int((packed.cpu().numpy() != e["q_packed"]).any(axis=2).sum())
+    e_gpu = xq.rel_mse(Wt, W_hat.cpu())
+    e_ref = xq.rel_mse(Wt, torch.from_numpy(e["q_W_hat"]))
+    print(f"vs golden: {diff_tiles}/64 tiles differ, rel MSE {e_gpu:.6e} vs {e_ref:.6e}",
+          flush=True)
+    assert diff_tiles <= 4
+    assert abs(e_gpu - e_ref) <= 1e-2 * e_ref
+
+
+def test_factor_hessian_fallback_on_device(xq):
+    """The damping fallback (quantize.py:815-835) on a device matrix that is
+    not positive definite: fp32 block LDL fails, fp64 with +0 and +0.1 x
+    mean(diag) fail, +1.0 x mean(diag) succeeds; the factor reproduces the
+    damped matrix and equals the CPU fallback's to fp64 rounding.  A
+    non-finite matrix raises."""
+    n = 256
+    g = torch.Generator().manual_seed(3)
+    Q, _ = torch.linalg.qr(torch.randn(n, n, generator=g, dtype=torch.float64))
+    lam = torch.ones(n, dtype=torch.float64)
+    lam[-1] = -0.5
+    G = (Q * lam) @ Q.t()
+    # the damping the fallback applies to the fp32 input taken to fp64:
+    # +0.1 x mean(diag), then +1.0 x the new mean(diag)
+    Gd = G.float().double()
+    Gd.diagonal().add_(0.1 * Gd.diagonal().mean())
+    Gd.diagonal().add_(1.0 * Gd.diagonal().mean())
+    out = []
+    for dev in ("cpu", "cuda"):
+        L = xq._factor_hessian(G.float().to(dev))
+        assert L.device.type == torch.device(dev).type
+        out.append(L.double().cpu())
+    assert float((out[1] - out[0]).norm() / out[0].norm()) < 1e-10
+    _, D = xq.block_LDL(Gd.clone().cuda(), 16)
+    L = out[1]
+    R = L @ torch.block_diag(*D.double().cpu()) @ L.t()
+    assert float((R - Gd).norm() / Gd.norm()) < 1e-10
+    bad = G.float().cuda()
+    bad[3, 5] = float("nan")
+    with pytest.raises(RuntimeError):
+        xq._factor_hessian(bad)
+
+
+def test_progress_sequence_matches_block_schedule(xq, monkeypatch):
+    """The column-chain schedule reports the reference's per-block progress
+    (quantize.py:666,732-734): progress(i, 512 * blocks done) for i = tk-1
+    .. 0, the same calls as the block schedule makes."""
+    g = torch.Generator().manual_seed(2)
+    W = (0.02 * torch.randn(128, 256, generator=g)).half().float()
+    H = _ar1_hessian(256, 512, 0.5, 2)
+    calls = {}
+    for sched in ("chain", "block"):
+        monkeypatch.setattr(xq, "DEFAULT_SCHEDULE", sched)
+        seen = []
+        xq.quantize_linear(W, H, K=4, device="cuda", margin=0,
+                           progress=lambda i, s, seen=seen: seen.append((i, s)))
+        calls[sched] = [c for c in seen if c[0] != "hinv"]
+    tk = 256 // 16
+    assert calls["chain"] == [(i, 512 * (tk - i)) for i in range(tk - 1, -1, -1)]
+    assert calls["chain"] == calls["block"]

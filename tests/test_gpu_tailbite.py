@@ -171,6 +171,35 @@ def test_batch_position_invariance(hb, K):
     assert ((st_all[:, 0] >> K) == (st_all[:, -1] & (SP - 1))).all()
 
 
+@pytest.mark.parametrize("K", (2, 4, 7))
+def test_forced_chunks(hb, oracle_mod, mul1_lut, K, monkeypatch):
+    """XTQ_VIT_SCRATCH is read on every call: a budget of 2048 sequences
+    splits a batch of 2 x 2048 + 700 into three chunks with a partial last
+    one (the full chunks take the separate-pass path with one-lane
+    tracebacks, the last the fused path).  Every tile equals the unchunked
+    run, and the first and last 32 tiles of each chunk equal the oracle."""
+    per = hb.scratch_per_seq(K)
+    rnd = 4 * torch.cuda.get_device_properties(0).multi_processor_count
+    ch = 2048 if 2048 <= rnd else 2048 - 2048 % rnd
+    n = 2 * 2048 + 700
+    rng = np.random.default_rng(40 + K)
+    X = torch.from_numpy(rng.standard_normal((n, 256)).astype(np.float32)).cuda()
+    monkeypatch.delenv("XTQ_VIT_SCRATCH", raising=False)
+    print(f"case K={K} n={n} unchunked", flush=True)
+    ref, ref_tr = hb.tailbite(X, K, 147, 16, trellis=True)
+    monkeypatch.setenv("XTQ_VIT_SCRATCH", str(2048 * per))
+    print(f"case K={K} n={n} chunks of {ch}", flush=True)
+    got, tr = hb.tailbite(X, K, 147, 16, trellis=True)
+    starts = list(range(0, n, ch))
+    assert len(starts) >= 3 and n - starts[-1] < ch
+    assert torch.equal(got, ref) and torch.equal(tr, ref_tr)
+    idx = sorted({i for c0 in starts for i in list(range(c0, c0 + 32)) +
+                  list(range(min(n, c0 + ch) - 32, min(n, c0 + ch)))})
+    want = oracle_mod.tailbite(X[idx].cpu().numpy(), mul1_lut, K, 16, pivot=147, margin=16,
+                               nthreads=len(os.sched_getaffinity(0)))
+    np.testing.assert_array_equal(got[idx].cpu().numpy(), want)
+
+
 @pytest.mark.parametrize("K", range(2, 8))
 def test_decode_unpack_pack(hb, oracle_mod, mul1_lut, K):
     """decode/unpack/pack kernels equal the oracle and the reference fixture."""
@@ -202,13 +231,20 @@ def test_nan_target_rejected(hb):
     assert st.shape == (2, 256)
 
 
-def test_valu_probe_rates(hb):
-    """The roofline probe runs and reports plausible rates: every probe
-    between 0.5x and 2.5x of one wave64 instruction per SIMD per 4 cycles."""
+def test_valu_probe_rates():
+    """The roofline probe (its own library) runs and reports plausible rates:
+    every probe between 0.5x and 2.5x of one wave64 instruction per SIMD per
+    4 cycles."""
+    import os
+    import sys
+    from conftest import PKG
+    if os.path.join(PKG, "probe") not in sys.path:
+        sys.path.insert(0, os.path.join(PKG, "probe"))
+    import valu_probe
     ncu = torch.cuda.get_device_properties(0).multi_processor_count
     base = ncu * 64 * 2.4e9
-    for i, name in enumerate(hb.VALU_PROBES):
-        r = hb.valu_probe(i)
+    for i, name in enumerate(valu_probe.PROBES):
+        r = valu_probe.rate(i)
         print(f"probe {name}: {r / 1e12:.2f} T/s", flush=True)
         assert 0.5 * base < r < 2.5 * base, (name, r)
 
@@ -281,6 +317,13 @@ def test_host_entry_matches_device(hb, mul1_lut):
     rc = hb.lib().xtq_vit_run(X.ctypes.data_as(ctypes.c_void_p), 5, b"ih2x2", 0, 128,
                               out.ctypes.data_as(ctypes.c_void_p))
     assert rc == 8
+    # a negative margin runs pass 1 over the whole sequence, as the
+    # reference kernel does (viterbi_esimd.cpp:413-414)
+    out3 = np.empty((5, 256), dtype=np.int32)
+    rc = hb.lib().xtq_vit_run(X.ctypes.data_as(ctypes.c_void_p), 5, b"mul1", -7, 128,
+                              out3.ctypes.data_as(ctypes.c_void_p))
+    assert rc == 0
+    np.testing.assert_array_equal(out3, _run(hb, X, 4, 128, 0)[0])
 
 
 def test_other_codebooks(hb, oracle_mod):
