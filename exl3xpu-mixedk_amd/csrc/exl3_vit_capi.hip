@@ -115,10 +115,23 @@ struct DevCtx {
     // the next call waits for it on its own stream, and growing the scratch
     // waits for it on the host before freeing.
     hipEvent_t last = nullptr;
+    // This device's copy of the no-allocation entry's scratch array (its
+    // address from hipGetSymbolAddress at set-up).
+    uint8_t* noalloc = nullptr;
 };
 
 std::mutex g_mu;
 std::vector<DevCtx> g_dev;
+
+// Device scratch of xtq_vit_tailbite_dev_noalloc: a file-scope array in the
+// code object, one copy per device, held until the process ends.  256 MiB
+// holds one call of up to 257 sequences at K=2 or 3, 513 at K=4 or 5, 1,027
+// at K=6 and 2,055 at K=7 (kNoAllocHeader bytes of status words, then the
+// per-sequence words and backpointer slots, see noalloc_capacity).  Host
+// code uses its per-device address (DevCtx::noalloc), never the name.
+constexpr size_t kNoAllocBytes = (size_t)256 << 20;
+constexpr size_t kNoAllocHeader = 256;
+static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
 
 // Opt-in kernel timing: each forward/traceback launch is bracketed with HIP
 // events on its stream; elapsed times are folded in after the stream syncs.
@@ -214,6 +227,13 @@ int dev_init(int dev) {
     if (hipMalloc((void**)&cx.counter, sizeof(int32_t)) != hipSuccess) return 2;
     if (hipEventCreateWithFlags(&cx.last, hipEventDisableTiming) != hipSuccess) return 1;
     if (hipEventRecord(cx.last, 0) != hipSuccess) return 1;
+    // this device's copy of the no-allocation scratch (the device is current)
+    void* na = nullptr;
+    if (hipGetSymbolAddress(&na, HIP_SYMBOL(scratch)) != hipSuccess || na == nullptr) {
+        fprintf(stderr, "xtq_vit: no device address for the no-allocation scratch\n");
+        return 1;
+    }
+    cx.noalloc = (uint8_t*)na;
     cx.owned = kNumCodes * 65536 * sizeof(uint16_t) + 256;
     cx.ready = true;
     return 0;
@@ -471,6 +491,63 @@ int run_tailbite(DevCtx& cx, const float* dX, int nseq, int K, Code code, int ma
                          s, true);
     if (rc) return rc;
     return scratch_end(cx, s, sync);
+}
+
+// --------------------------------------------- tail-bite without allocation
+// Sequences of K one call of the no-allocation entry can take: a header,
+// three words per sequence, up to 255 bytes of alignment, and the
+// backpointer slots.
+size_t noalloc_capacity(int K) {
+    return (kNoAllocBytes - kNoAllocHeader - 256) / (xtq::bp_tile_bytes(K) + 3 * sizeof(int32_t));
+}
+
+// xtq_vit_tailbite_dev over the device's copy of `scratch` (its address in
+// cx.noalloc, taken once at set-up): no allocation, one chunk, synchronous.
+int run_tailbite_noalloc(DevCtx& cx, const float* dX, int nseq, int K, Code code, int margin,
+                         int pivot, int32_t* d_states, int16_t* d_trellis, hipStream_t s) {
+    const size_t cap = noalloc_capacity(K);
+    if ((size_t)nseq > cap) {
+        fprintf(stderr, "xtq_vit: nseq %d exceeds the no-allocation scratch (%zu sequences at "
+                "K=%d)\n", nseq, cap, K);
+        return 5;
+    }
+    uint8_t* base = cx.noalloc;
+    TbScratch w;
+    w.err = (uint32_t*)base;
+    w.counter = (int32_t*)(base + 4);
+    w.send = (int32_t*)(base + kNoAllocHeader);
+    w.ov = w.send + nseq;
+    w.flags = (uint32_t*)(w.ov + nseq);
+    const uintptr_t bp = ((uintptr_t)(w.flags + nseq) + 255) & ~(uintptr_t)255;
+    w.bp = (void*)bp;
+    if (bp + (size_t)nseq * xtq::bp_tile_bytes(K) > (uintptr_t)(base + kNoAllocBytes)) return 5;
+    // The array keeps the previous call's contents: the status word and the
+    // fused kernel's ready flags must start at zero (epochs start at 1).
+    hipError_t e = xtq::launch_fill_u32(w.err, 1, 0u, s);
+    if (e == hipSuccess) e = xtq::launch_fill_u32(w.flags, (uint32_t)nseq, 0u, s);
+    if (e != hipSuccess) {
+        fprintf(stderr, "xtq_vit run: %s\n", hipGetErrorString(e));
+        return 4;
+    }
+    int rc = tailbite_chunks(cx, w, nseq, dX, nseq, K, code, margin, pivot, d_states,
+                             d_trellis, s, false);
+    if (rc) return rc;
+    uint32_t herr = 0;
+    if (hipMemcpyAsync(&herr, w.err, sizeof(herr), hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess) {
+        fprintf(stderr, "xtq_vit run: %s\n", hipGetErrorString(hipGetLastError()));
+        return 4;
+    }
+    if (herr & 6u) {
+        fprintf(stderr, "xtq_vit: persistent kernel %s\n",
+                (herr & 2u) ? "wait expired" : "task out of range");
+        return 4;
+    }
+    if (herr) {
+        fprintf(stderr, "xtq_vit: NaN target\n");
+        return 11;
+    }
+    return 0;
 }
 
 // Relative cost of one tile of the chain kernel per K, for splitting the CUs
@@ -798,6 +875,31 @@ int xtq_vit_tailbite_dev_async(const float* dX, int nseq, int K, const char* cod
                                int margin, int pivot, int32_t* d_states, int16_t* d_trellis,
                                void* stream) {
     return tailbite_dev(dX, nseq, K, code, margin, pivot, d_states, d_trellis, stream, false);
+}
+
+int xtq_vit_tailbite_dev_noalloc(const float* dX, int nseq, int K, const char* code,
+                                 int margin, int pivot, int32_t* d_states, int16_t* d_trellis,
+                                 void* stream) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!dX || (!d_states && !d_trellis)) return 12;
+    Code c;
+    int rc = parse_code(code, &c);
+    if (rc) return rc;
+    read_env();
+    if (nseq <= 0) return 6;
+    rc = check_args(K, margin, pivot);
+    if (rc) return rc;
+    int dev = 0;
+    if (current_device(&dev)) return 1;
+    // Setting a device up allocates (codebook tables, status words): that is
+    // the init call's job, never this entry's.
+    if (dev >= (int)g_dev.size() || !g_dev[dev].ready) {
+        fprintf(stderr, "xtq_vit: device %d is not set up; call xtq_vit_init (or any other "
+                "entry point) on it before xtq_vit_tailbite_dev_noalloc\n", dev);
+        return 1;
+    }
+    return run_tailbite_noalloc(g_dev[dev], dX, nseq, K, c, margin, pivot, d_states, d_trellis,
+                                (hipStream_t)stream);
 }
 
 int xtq_vit_status_dev(void* stream) {

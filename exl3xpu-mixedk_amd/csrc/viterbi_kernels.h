@@ -114,4 +114,7 @@ hipError_t launch_pack(int K, const int32_t* states, int nt, int16_t* trellis,
 hipError_t launch_unpack(int K, const int16_t* trellis, int nt, int32_t* states,
                          hipStream_t stream);
 
+// p[0..n) = v on `stream` (a kernel, so that it may be captured in a graph).
+hipError_t launch_fill_u32(uint32_t* p, uint32_t n, uint32_t v, hipStream_t stream);
+
 }  // namespace xtq

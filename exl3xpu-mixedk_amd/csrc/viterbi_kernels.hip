@@ -811,6 +811,12 @@ __global__ __launch_bounds__(kFwdThreads) void tailbite_fused_kernel(
 // the sequence stays capturable in a HIP graph).
 __global__ void reset_counter_kernel(int32_t* counter) { *counter = 0; }
 
+// p[0..n) = v, one word per thread (flags and status words of reused
+// scratch; a kernel rather than a memset, as above).
+__global__ void fill_u32_kernel(uint32_t* __restrict__ p, uint32_t n, uint32_t v) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i < n) p[i] = v;
+}
 
 // ------------------------------------------------- decode / pack / unpack
 // tensor_core_perm (quantize.py:101-118): element t -> row-major 16x16 index.
@@ -1388,6 +1394,13 @@ hipError_t launch_unpack(int K, const int16_t* trellis, int nt, int32_t* states,
                          hipStream_t stream) {
     if (nt <= 0) return hipSuccess;
     return dispatch_k<UnpackL>(K, trellis, nt, states, stream);
+}
+
+hipError_t launch_fill_u32(uint32_t* p, uint32_t n, uint32_t v, hipStream_t stream) {
+    if (n == 0) return hipSuccess;
+    if (p == nullptr) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(fill_u32_kernel, dim3((n + 255u) / 256u), dim3(256), 0, stream, p, n, v);
+    return hipGetLastError();
 }
 
 #endif  // XTQ_FWD_K3_TU

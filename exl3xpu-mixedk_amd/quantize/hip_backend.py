@@ -51,6 +51,7 @@ def lib():
         L.xtq_vit_run_k.argtypes = [vp, i32, i32, cp, i32, i32, vp]
         L.xtq_vit_tailbite_dev.argtypes = [vp, i32, i32, cp, i32, i32, vp, vp, vp]
         L.xtq_vit_tailbite_dev_async.argtypes = [vp, i32, i32, cp, i32, i32, vp, vp, vp]
+        L.xtq_vit_tailbite_dev_noalloc.argtypes = [vp, i32, i32, cp, i32, i32, vp, vp, vp]
         L.xtq_vit_status_dev.argtypes = [vp]
         L.xtq_ldlq_chain_dev.argtypes = [vp, vp, i32, i32, i32, cp, i32, i32, vp, vp, vp, vp, vp]
         L.xtq_ldlq_chain_multi_dev.argtypes = [vp, vp, i32, i32, i32, vp, vp, cp, i32, i32,
@@ -71,7 +72,7 @@ def lib():
         L.xtq_vit_strerror.argtypes = [i32]
         L.xtq_vit_strerror.restype = cp
         for fn in ("xtq_vit_init", "xtq_vit_run", "xtq_vit_run_k", "xtq_vit_tailbite_dev",
-                   "xtq_vit_tailbite_dev_async", "xtq_vit_status_dev", "xtq_vit_viterbi_dev",
+                   "xtq_vit_tailbite_dev_async", "xtq_vit_tailbite_dev_noalloc", "xtq_vit_status_dev", "xtq_vit_viterbi_dev",
                    "xtq_ldlq_chain_dev", "xtq_ldlq_chain_multi_dev",
                    "xtq_trellis_decode_dev", "xtq_trellis_pack_dev",
                    "xtq_trellis_unpack_dev", "xtq_vit_get_lut"):

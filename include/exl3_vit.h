@@ -131,6 +131,25 @@ XTQ_API int xtq_vit_tailbite_dev_async(const float* dX, int nseq, int K, const c
                                int16_t* d_trellis, void* stream);
 
 /*
+ * xtq_vit_tailbite_dev without any device allocation.  No reference
+ * counterpart: for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The caller passes inputs and outputs as for xtq_vit_tailbite_dev; the
+ * backpointers and per-sequence words live in a fixed 256 MiB array in the
+ * library's code object (one copy per device, held until the process ends),
+ * so one call takes at most 257 sequences at K=2 or 3, 513 at K=4 or 5,
+ * 1,027 at K=6 and 2,055 at K=7 (status 5 beyond that; split the batch).
+ * The device must have been set up by xtq_vit_init (or by any other entry
+ * point) first, else status 1.  Synchronous; calls are serialised by the
+ * library's lock, and since each returns only after its work has finished,
+ * calls on one GPU never overlap (each process has its own array).
+ * Results equal xtq_vit_tailbite_dev's bit for bit.
+ */
+XTQ_API int xtq_vit_tailbite_dev_noalloc(const float* dX, int nseq, int K, const char* code,
+                                         int margin, int pivot, int32_t* d_states,
+                                         int16_t* d_trellis, void* stream);
+
+/*
  * Waits for `stream` and reports the NaN flag that stream-ordered encodes
  * set since the last status or synchronous call: 0, or 11 (the flag is then
  * cleared), or 4 on a HIP error.
