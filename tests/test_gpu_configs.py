@@ -12,7 +12,8 @@ Every tile of every run:
     through the incoherence transform, equal quantize_linear's W_hat bit for
     bit (quantize.py:852-853, 862-866).
 Sampled block rows spread over the sweep (the first row swept, which has no
-feedback, the last, which has the most, and rows between): every tile's
+feedback, the last, which has the most, and rows between; 8 rows, 16 for
+c2): every tile's
 states bit for bit against the C oracle on the targets the kernel computed
 (the reference's per-launch dual method, quantize.py:687-717).  The batched
 workload checks the first and last 64 tiles of every scratch chunk the
@@ -135,7 +136,7 @@ def _run_config(xq, hb, O, Ws, H, Ks, cs, rows_per_run, label):
 def test_c2_full_size(xq, hb, wl, oracle_mod):
     print("case c2 4096x4096 K=4", flush=True)
     w = wl.c2(device="cuda")
-    _run_config(xq, hb, oracle_mod, [w["W"]], w["H"], 4, False, 6, "c2")
+    _run_config(xq, hb, oracle_mod, [w["W"]], w["H"], 4, False, 16, "c2")
 
 
 @pytest.fixture(scope="module")
@@ -148,14 +149,14 @@ def c3(wl):
 @pytest.mark.parametrize("K", range(2, 8))
 def test_c3_full_size(xq, hb, c3, oracle_mod, K):
     print(f"case c3 5120x5120 K={K}", flush=True)
-    _run_config(xq, hb, oracle_mod, [c3["W"]], c3["H"], K, False, 4, f"c3 K={K}")
+    _run_config(xq, hb, oracle_mod, [c3["W"]], c3["H"], K, False, 8, f"c3 K={K}")
 
 
 def test_c4_full_size(xq, hb, wl, oracle_mod):
     print("case c4 qkv K=[5,7,7] channel scales", flush=True)
     w = wl.c4(device="cuda")
     Ks = [m["K"] for m in w["members"]]
-    _run_config(xq, hb, oracle_mod, [m["W"] for m in w["members"]], w["H"], Ks, True, 4,
+    _run_config(xq, hb, oracle_mod, [m["W"] for m in w["members"]], w["H"], Ks, True, 8,
                 "c4")
 
 
@@ -169,7 +170,7 @@ def c5(wl):
 @pytest.mark.parametrize("K", (6, 4))
 def test_c5_full_size(xq, hb, c5, oracle_mod, K):
     print(f"case c5 5120x17408 K={K}", flush=True)
-    _run_config(xq, hb, oracle_mod, [c5["W"]], c5["H"], K, False, 4, f"c5 K={K}")
+    _run_config(xq, hb, oracle_mod, [c5["W"]], c5["H"], K, False, 8, f"c5 K={K}")
 
 
 def _chunk_rows(hb, K: int, nseq: int, budget: int = 8 << 30) -> int:
@@ -187,7 +188,7 @@ def test_headline_batch_every_chunk(hb, wl, oracle_mod):
     """The benchmark's 348,160 independent K=4 tiles in one call: every tile's
     wrap invariant and pack round trip; the first and last 64 tiles of every
     scratch chunk (the chunk loop's offsets into targets, states and trellis,
-    and the partial last chunk) and 512 random tiles against the oracle."""
+    and the partial last chunk) and 4,096 random tiles against the oracle."""
     monkey = os.environ.pop("XTQ_VIT_SCRATCH", None)
     try:
         print("case headline 348160 tiles K=4 pivot 128 margin 0", flush=True)
@@ -206,7 +207,7 @@ def test_headline_batch_every_chunk(hb, wl, oracle_mod):
             idx.update(range(c0, c0 + 64))
             idx.update(range(c1 - 64, c1))
         rng = np.random.default_rng(0)
-        idx.update(rng.choice(n, 512, replace=False).tolist())
+        idx.update(rng.choice(n, 4096, replace=False).tolist())
         idx = np.array(sorted(idx))
         lut = oracle_mod.code_lut("exl3_mul1")
         want = oracle_mod.tailbite(X[torch.from_numpy(idx).cuda()].cpu().numpy(), lut, 4, 16,
