@@ -183,10 +183,13 @@ void prof_collect() {
 //                       -> status 5
 //     XTQ_VIT_SCRATCH   backpointer scratch budget; larger batches run in
 //                       chunks (default 8 GiB)
+//     XTQ_VIT_DEFER_SCRATCH  the same for the deferred-argmin encode's minima
+//                       rows (default 48 GiB, at most half the free memory)
 long long g_host_maxseq = 4096;
 size_t g_host_maxbytes = (size_t)6 << 30;
 size_t g_maxbytes = (size_t)64 << 30;
 size_t g_scratch = (size_t)8 << 30;
+size_t g_defer_scratch = (size_t)48 << 30;
 // Worst-case device bytes per sequence of the reference's library (X 1 KiB,
 // states 1 KiB, cost table 256 KiB, backpointers 1 MiB).
 constexpr size_t kRefBytesPerSeq = 1317888;
@@ -199,6 +202,8 @@ void read_env() {
     g_maxbytes = (e = getenv("XTQ_VIT_DEV_MAXBYTES")) ? strtoull(e, nullptr, 10)
                                                       : (size_t)64 << 30;
     g_scratch = (e = getenv("XTQ_VIT_SCRATCH")) ? strtoull(e, nullptr, 10) : (size_t)8 << 30;
+    g_defer_scratch = (e = getenv("XTQ_VIT_DEFER_SCRATCH")) ? strtoull(e, nullptr, 10)
+                                                             : (size_t)48 << 30;
 }
 
 // Makes `dev` ready on the calling thread (which must have it current).
@@ -284,10 +289,29 @@ int check_args(int K, int margin, int pivot) {
     return 0;
 }
 
+// Scratch bytes per sequence: packed backpointers, or the minima rows of
+// the deferred-argmin forward.
+size_t scratch_per_seq(int K, bool defer) {
+    return defer ? xtq::defer_tile_bytes(K) : xtq::bp_tile_bytes(K);
+}
+
 // Sequences per chunk for a scratch budget.
-int chunk_size(const DevCtx& cx, int K, int nseq) {
-    const size_t per = xtq::bp_tile_bytes(K);
-    size_t ch = g_scratch / per;
+int chunk_size(const DevCtx& cx, int K, int nseq, bool defer = false) {
+    const size_t per = scratch_per_seq(K, defer);
+    size_t budget = g_scratch;
+    if (defer) {
+        // the minima rows take 8x the backpointers' bytes at K=4: a larger
+        // budget keeps the chunks (each one latency-bound traceback launch
+        // per pass) at thousands of sequences, capped at half of the device
+        // memory this library could hold
+        budget = g_defer_scratch;
+        size_t fr = 0, tot = 0;
+        if (hipMemGetInfo(&fr, &tot) == hipSuccess) {
+            const size_t avail = (fr + cx.bp_cap) / 2;
+            if (budget > avail) budget = avail;
+        }
+    }
+    size_t ch = budget / per;
     if (ch < 1) ch = 1;
     const size_t round = (size_t)4 * (cx.ncu > 0 ? cx.ncu : 1);
     if (ch > round) ch -= ch % round;
@@ -296,8 +320,8 @@ int chunk_size(const DevCtx& cx, int K, int nseq) {
 }
 
 // Grows the backpointer/final-state scratch for `chunk` sequences of K.
-int reserve_scratch(DevCtx& cx, int K, int chunk) {
-    const size_t per = xtq::bp_tile_bytes(K);
+int reserve_scratch(DevCtx& cx, int K, int chunk, bool defer = false) {
+    const size_t per = scratch_per_seq(K, defer);
     // A stream-ordered call may still be using the buffers about to be
     // replaced.
     if (((size_t)chunk * per > cx.bp_cap || (size_t)chunk > cx.seq_cap) &&
@@ -394,6 +418,18 @@ bool use_lanes(int n) {
     return min_n >= 0 && n >= min_n;
 }
 
+// Whether a tail-bite at K runs the deferred-argmin forward (group minima
+// rows in HBM, argmin recomputed by the traceback): XTQ_VIT_DEFER=1 for
+// K >= 4, else never.  Measured on the 348,160-tile K=4..7 workloads it is
+// 3-4 % slower end to end: its forward gains 3-9 %, its one-lane
+// tracebacks recomputing NC candidates per link cost more.
+bool use_defer(int K, int nseq) {
+    (void)nseq;
+    if (K < 4) return false;
+    const char* e = getenv("XTQ_VIT_DEFER");
+    return e && !strcmp(e, "1");
+}
+
 // Polls before a pass-2 wait in the fused kernel gives up (~1 us each, so
 // seconds; a pass-1 task takes about a millisecond).
 constexpr int kSpinLimit = 1 << 22;
@@ -415,7 +451,7 @@ struct TbScratch {
 // launches with timing events (the benchmark's kernel timing).
 int tailbite_chunks(DevCtx& cx, const TbScratch& w, int chunk, const float* dX, int nseq,
                     int K, Code code, int margin, int pivot, int32_t* d_states,
-                    int16_t* d_trellis, hipStream_t s, bool prof) {
+                    int16_t* d_trellis, hipStream_t s, bool prof, bool defer = false) {
     const int n1 = (margin > 0 && pivot + margin < xtq::kSteps) ? pivot + margin : xtq::kSteps;
     const uint16_t* lut = cx.lut16[code];
     auto pbeg = [&](int kind, double steps) { return prof ? prof_begin(s, kind, steps) : -1; };
@@ -426,6 +462,39 @@ int tailbite_chunks(DevCtx& cx, const TbScratch& w, int chunk, const float* dX, 
         int16_t* tr = d_trellis ? d_trellis + (size_t)c0 * 16 * K : nullptr;
         const int T = pick_group(cx, K, n);
         hipError_t e;
+        if (defer) {
+            // Pass 1, free on the rolled sequence: minima rows from step
+            // pivot, traced back to ov = s_pivot >> K; pass 2 pinned to ov.
+            int pf = pbeg(0, (double)n * n1);
+            e = xtq::launch_forward_defer(K, x, xtq::kSteps, xtq::kSteps, n, lut, pivot, n1,
+                                          pivot, nullptr, w.bp, w.send, w.err, T, s);
+            prof_end(pf, s);
+            if (e == hipSuccess) {
+                pf = pbeg(1, 0.0);
+                e = xtq::launch_traceback_defer(K, w.bp, x, xtq::kSteps, xtq::kSteps, pivot, lut,
+                                                n, w.send, nullptr, n1, pivot, K, w.ov, nullptr,
+                                                nullptr, s);
+                prof_end(pf, s);
+            }
+            if (e == hipSuccess) {
+                pf = pbeg(0, (double)n * xtq::kSteps);
+                e = xtq::launch_forward_defer(K, x, xtq::kSteps, xtq::kSteps, n, lut, 0,
+                                              xtq::kSteps, 0, w.ov, w.bp, w.send, w.err, T, s);
+                prof_end(pf, s);
+            }
+            if (e == hipSuccess) {
+                pf = pbeg(1, 0.0);
+                e = xtq::launch_traceback_defer(K, w.bp, x, xtq::kSteps, xtq::kSteps, 0, lut, n,
+                                                w.send, w.ov, xtq::kSteps, 0, 0, nullptr, st,
+                                                tr, s);
+                prof_end(pf, s);
+            }
+            if (e != hipSuccess) {
+                fprintf(stderr, "xtq_vit run: %s\n", hipGetErrorString(e));
+                return 4;
+            }
+            continue;
+        }
         if (use_fused(cx, n)) {
             if (++cx.epoch == 0) cx.epoch = 1;
             int pf = pbeg(0, (double)n * (n1 + xtq::kSteps));
@@ -482,13 +551,14 @@ int tailbite_chunks(DevCtx& cx, const TbScratch& w, int chunk, const float* dX, 
 int run_tailbite(DevCtx& cx, const float* dX, int nseq, int K, Code code, int margin,
                  int pivot, int32_t* d_states, int16_t* d_trellis, hipStream_t s,
                  bool sync = true) {
-    const int chunk = chunk_size(cx, K, nseq);
-    int rc = reserve_scratch(cx, K, chunk);
+    const bool defer = use_defer(K, nseq);
+    const int chunk = chunk_size(cx, K, nseq, defer);
+    int rc = reserve_scratch(cx, K, chunk, defer);
     if (!rc) rc = scratch_begin(cx, s);
     if (rc) return rc;
     const TbScratch w{cx.bp, cx.send, cx.ov, cx.flags, cx.counter, cx.err};
     rc = tailbite_chunks(cx, w, chunk, dX, nseq, K, code, margin, pivot, d_states, d_trellis,
-                         s, true);
+                         s, true, defer);
     if (rc) return rc;
     return scratch_end(cx, s, sync);
 }
@@ -1036,6 +1106,20 @@ int xtq_vit_get_lut(const char* code, float* out) {
 int64_t xtq_vit_scratch_per_seq(int K) {
     if (K < 2 || K > 7) return -1;
     return (int64_t)xtq::bp_tile_bytes(K);
+}
+
+int xtq_vit_chunk_seqs(int nseq, int K, int* deferred) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (nseq <= 0) return -6;
+    if (K < 2 || K > 7) return -9;
+    read_env();
+    int dev = 0;
+    if (current_device(&dev)) return -1;
+    const int rc = dev_init(dev);
+    if (rc) return -rc;
+    const bool defer = use_defer(K, nseq);
+    if (deferred) *deferred = defer ? 1 : 0;
+    return chunk_size(g_dev[dev], K, nseq, defer);
 }
 
 int xtq_vit_prof_enable(int on) {

@@ -51,6 +51,26 @@ hipError_t launch_forward_k3(const float* X, int xstride, int xlen, int nseq,
                              const int32_t* ov_in, void* bp, int32_t* send, uint32_t* err,
                              int group, hipStream_t stream);
 
+// The forward DP with the argmin deferred to the traceback (K >= 4): same
+// arguments as launch_forward, but instead of packed backpointers it writes
+// the group minima b_r of steps r = max(store_lo, 1) .. nsteps-2 to bm, one
+// row of 2^(16-K) floats per step, defer_tile_bytes(K) per sequence.
+size_t defer_tile_bytes(int K);
+hipError_t launch_forward_defer(int K, const float* X, int xstride, int xlen, int nseq,
+                                const uint16_t* lut16, int roll, int nsteps, int store_lo,
+                                const int32_t* ov_in, void* bm, int32_t* send, uint32_t* err,
+                                int group, hipStream_t stream);
+
+// Traceback of launch_forward_defer's run from send down to step `stop`
+// (one lane per sequence), recomputing each link's argmin from the minima
+// rows, the codebook and the targets (X, xstride, xlen, roll as the forward
+// read them; ov_in the run's pins or NULL).  Outputs as launch_traceback.
+hipError_t launch_traceback_defer(int K, const void* bm, const float* X, int xstride, int xlen,
+                                  int roll, const uint16_t* lut16, int nseq,
+                                  const int32_t* send, const int32_t* ov_in, int nsteps,
+                                  int stop, int shift, int32_t* sout, int32_t* states,
+                                  int16_t* trellis, hipStream_t stream);
+
 // Both tail-biting passes of nseq sequences (256-step targets X [nseq][256])
 // in one launch of 2*nseq workgroups (see tailbite_fused_kernel): pass 1
 // free on X rolled by pivot for n1 steps, traced back in-kernel to

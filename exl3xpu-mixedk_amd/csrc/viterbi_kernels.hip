@@ -37,6 +37,7 @@
 
 #pragma clang fp contract(off)
 
+
 namespace xtq {
 namespace {
 
@@ -733,6 +734,349 @@ __global__ __launch_bounds__(kTbLaneSeqs) void tb_lane_kernel(
     }
 }
 
+// ------------------------------------------------- deferred-argmin encode
+// The batched forward of fwd_run without the argmin: its min tree takes the
+// group minima of the fp32 costs alone (v_min3_f32 / v_min_f32, half an
+// instruction per candidate against fwd_run's v_min_f64 on a 64-bit
+// (cost, index) key), and each step's minima b_{i+1} go to LDS for the next
+// step and, for steps store_lo .. nsteps-2, to HBM: one row of SP floats per
+// step in `bm` (Geom<K>::SP * 4 bytes, kSlots rows per sequence, row r
+// holding b_r).  The traceback (tb_defer_kernel) then recomputes, for the one
+// group on the path at each link, the costs of its NC candidates from b_{i-1},
+// the codebook and x_{i-1} with the forward's own fp32 operations, and takes
+// the first index of their minimum -- the reference's tie rule
+// (quantize.py:288-292,316-319).  The final state (the argmin of the last
+// step) is found after the step loop from b_{nsteps-1}, which stays in LDS.
+//
+// Worth it where the minima rows are small enough to write: SP * 4 bytes per
+// tile-step is 16 KiB at K=4 (8 times the packed backpointers) and 2 KiB at
+// K=7; K = 2, 3 would write 64 / 32 KiB per tile-step, more than HBM takes at
+// the forward's rate, so they keep fwd_run.
+__device__ __forceinline__ float fmin2(float a, float b) {
+    float r;
+    asm("v_min_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+__device__ __forceinline__ float fmin3(float a, float b, float c) {
+    float r;
+    asm("v_min3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
+// Minimum of v[0..N) (costs are never NaN: a NaN target ends the call with
+// status 11, and IEEE min needs no canonicalisation here), in triples
+// (a v_min_f32 pair tree measured 3-7 % slower).
+template <int N>
+__device__ __forceinline__ float min_tree(const float* v) {
+    if constexpr (N == 1) {
+        return v[0];
+    } else if constexpr (N == 2) {
+        return fmin2(v[0], v[1]);
+    } else if constexpr (N == 3) {
+        return fmin3(v[0], v[1], v[2]);
+    } else {
+        constexpr int M = (N + 2) / 3;
+        float r[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            if (3 * m + 2 < N) r[m] = fmin3(v[3 * m], v[3 * m + 1], v[3 * m + 2]);
+            else if (3 * m + 1 < N) r[m] = fmin2(v[3 * m], v[3 * m + 1]);
+            else r[m] = v[3 * m];
+        }
+        return min_tree<M>(r);
+    }
+}
+
+// Minima rows kept per sequence (row r holds b_r, r = 1 .. 254) and their
+// bytes per sequence.
+template <int K>
+constexpr size_t defer_tile_bytes() {
+    return (size_t)kSlots * Geom<K>::SP * sizeof(float);
+}
+
+// Forward DP of sequences q0 .. q0+ntile-1 by one 1024-thread workgroup with
+// the argmin deferred to the traceback (see above).  Arguments as fwd_run,
+// with bm the minima rows (defer_tile_bytes<K>() per sequence).
+template <int K, int T>
+__device__ __forceinline__ void fwd_run_defer(
+    FwdSmem<K, T>& sm, const float* __restrict__ X, int xstride, int xlen, int q0, int ntile,
+    const uint16_t* __restrict__ lut16, int roll, int nsteps, int store_lo, bool pinned,
+    float* __restrict__ bm, int32_t* send, uint32_t* __restrict__ err, int tid) {
+    using G = Geom<K>;
+    static_assert(K >= 4, "K = 2, 3 keep the key-argmin forward");
+    static_assert(G::NB == 1, "one predecessor block per thread");
+    auto& bbuf = sm.bbuf;
+    auto& xs = sm.xs;
+    auto& ovs = sm.ovs;
+    auto& red = sm.red;
+
+#pragma unroll
+    for (int r0 = 0; r0 < T * kSteps; r0 += kFwdThreads) {
+        if (r0 + kFwdThreads <= T * kSteps || tid < T * kSteps - r0) {
+            const int idx = r0 + tid, tt = idx / kSteps, e = idx % kSteps;
+            float v = 0.0f;
+            if (tt < ntile && e < xlen) {
+                v = X[(size_t)(q0 + tt) * xstride + e];
+                if (v != v) atomicOr(err, 1u);
+            }
+            xs[tt][e] = v;
+        }
+    }
+
+    const int jbase = G::HALF ? (tid >> 1) : tid * G::C;
+    const int wbase = G::HALF ? (tid & 1) * G::W : 0;
+    constexpr int NCH = kChunkW<K, T>;
+    constexpr int NCHUNK = G::W / NCH;
+    float f32[G::NSTATE];
+#pragma unroll
+    for (int l = 0; l < G::NSTATE; ++l)
+        f32[l] = (float)__builtin_bit_cast(
+            _Float16, lut16[jbase + l / G::W + (wbase + l % G::W) * G::SP]);
+    auto fsub = [&](int l, float negx) { return f32[l] + negx; };
+    __syncthreads();
+
+    for (int tt = 0; tt < T; ++tt) {
+        const int ov = ovs[tt];
+        if (!G::HALF || (tid & 1) == 0) {
+#pragma unroll
+            for (int c = 0; c < G::C; ++c) {
+                const int j = jbase + c;
+                bbuf[tt][0][bslot<K>(j)] = (ov < 0 || j == ov) ? 0.0f : __builtin_inff();
+            }
+        }
+    }
+    __syncthreads();
+
+    const int a0 = jbase >> K;
+    const int rpad = bslot<K>(a0 + wbase * G::Q) - (a0 + wbase * G::Q);
+    // b_{i+1} of the last step is never stored (the final state is found
+    // from LDS below); rows store_lo .. nsteps-2 are
+    const int last_row = nsteps - 2;
+    for (int i = 0; i + 1 < nsteps; ++i) {
+        const int u = (i - roll < 0) ? i - roll + xlen : i - roll;
+#pragma unroll 1
+        for (int tt = 0; tt < ntile; ++tt) {
+#pragma unroll
+            for (int l = 0; l < G::NSTATE; ++l) asm volatile("" : "+v"(f32[l]));
+            const int q = q0 + tt;
+            const float negx = -__int_as_float(
+                __builtin_amdgcn_readfirstlane(__float_as_int(xs[tt][u])));
+            const float* bcur = bbuf[tt][i & 1];
+            float run[G::C];
+#pragma unroll
+            for (int qc = 0; qc < NCHUNK; ++qc) {
+                float B[G::NB][NCH];
+#pragma unroll
+                for (int w = 0; w < NCH; ++w) {
+                    const float* src = bcur + a0 + rpad + (wbase + qc * NCH + w) * G::Q;
+                    B[0][w] = src[0];
+                }
+#pragma unroll
+                for (int c = 0; c < G::C; ++c) {
+                    constexpr int U = T * NCHUNK * G::C;
+                    const int pos = (tt * NCHUNK + qc) * G::C + c;
+                    constexpr int D1 = K >= 5 ? U * 5 / 8 : T == 1 ? U / 4 : U / 2;
+                    constexpr int D0 = K >= 5 ? U * 7 / 8 : K == 4 && T == 1 ? U * 5 / 8
+                                                                              : U * 3 / 4;
+                    if (pos == D1) __builtin_amdgcn_s_setprio(1);
+                    if (pos == D0) __builtin_amdgcn_s_setprio(0);
+                    float dv[NCH];
+                    if constexpr (kGroupOps<K, T>) {
+#pragma unroll
+                        for (int w = 0; w < NCH; ++w) dv[w] = fsub(c * G::W + qc * NCH + w, negx);
+#pragma unroll
+                        for (int w = 0; w < NCH; ++w) asm volatile("" : "+v"(dv[w]));
+#pragma unroll
+                        for (int w = 0; w < NCH; ++w) dv[w] = dv[w] * dv[w];
+#pragma unroll
+                        for (int w = 0; w < NCH; ++w) asm volatile("" : "+v"(dv[w]));
+#pragma unroll
+                        for (int w = 0; w < NCH; ++w) dv[w] = dv[w] + B[0][w];
+                    } else {
+#pragma unroll
+                        for (int w = 0; w < NCH; ++w) {
+                            const float d = fsub(c * G::W + qc * NCH + w, negx);
+                            dv[w] = d * d + B[0][w];
+                        }
+                    }
+                    const float m = min_tree<NCH>(dv);
+                    run[c] = (qc == 0) ? m : fmin2(run[c], m);
+                }
+            }
+            if constexpr (G::HALF) {
+                // merge the two halves of the group (lanes 2t, 2t+1) with a
+                // DPP quad permutation [1,0,3,2]
+                const float o = __int_as_float(__builtin_amdgcn_mov_dpp(
+                    __float_as_int(run[0]), 0xB1, 0xF, 0xF, false));
+                run[0] = fmin2(run[0], o);
+            }
+            float* bnext = bbuf[tt][(i + 1) & 1] + bslot<K>(jbase);
+            if constexpr (G::C == 4) {
+                *(float4*)bnext = make_float4(run[0], run[1], run[2], run[3]);
+            } else if constexpr (G::C == 2) {
+                *(float2*)bnext = make_float2(run[0], run[1]);
+            } else {
+                if (!G::HALF || (tid & 1) == 0) bnext[0] = run[0];
+            }
+            if (i + 1 >= store_lo && i + 1 <= last_row) {
+                // row i+1 of this sequence: a wave-uniform base plus the
+                // lane's offset; streamed past the caches (read back only by
+                // the traceback, after the launch)
+                gbyte_t* const row = uniform_gptr(
+                    (uint8_t*)(bm + ((size_t)q * kSlots + (size_t)(i + 1)) * G::SP));
+                gbyte_t* const dst = row + (uint32_t)jbase * 4u;
+                typedef float v4f __attribute__((ext_vector_type(4)));
+                typedef float v2f __attribute__((ext_vector_type(2)));
+                if constexpr (G::C == 4) {
+                    const v4f v = {run[0], run[1], run[2], run[3]};
+                    __builtin_nontemporal_store(v, (__attribute__((address_space(1))) v4f*)dst);
+                } else if constexpr (G::C == 2) {
+                    const v2f v = {run[0], run[1]};
+                    __builtin_nontemporal_store(v, (__attribute__((address_space(1))) v2f*)dst);
+                } else {
+                    if (!G::HALF || (tid & 1) == 0)
+                        __builtin_nontemporal_store(
+                            run[0], (__attribute__((address_space(1))) float*)dst);
+                }
+            }
+        }
+        __syncthreads();
+        __builtin_amdgcn_s_setprio(kPrioTop<K>);
+    }
+    __builtin_amdgcn_s_setprio(0);
+
+    // The last step: c[s] = fl(fl(fl(f[s] - x)^2) + b_{nsteps-1}[s >> K]), then
+    // the final state -- pinned: the first minimum among the states with
+    // s mod SP == ov (state 0 when every allowed cost is +inf,
+    // quantize.py:298-306); free: the lowest state index among the minimum
+    // costs (quantize.py:306,315).  Thread t takes states t + 1024 k with the
+    // codebook read from the table (its registers are free by now) and
+    // (cost, state) 64-bit keys, whose fp64 order is the lexicographic one.
+    const int ul = (nsteps - 1 - roll < 0) ? nsteps - 1 - roll + xlen : nsteps - 1 - roll;
+    for (int tt = 0; tt < ntile; ++tt) {
+        const float negx = -xs[tt][ul];
+        const float* bcur = bbuf[tt][(nsteps - 1) & 1];
+        const int ov = ovs[tt];
+        double best = key_of(0xFFFFFFFFu, __builtin_inff());
+#pragma unroll 8
+        for (int k = 0; k < 65536 / kFwdThreads; ++k) {
+            const int st_ = tid + k * kFwdThreads;
+            const float f = (float)__builtin_bit_cast(_Float16, lut16[st_]);
+            const float d = f + negx;
+            const float cost = d * d + bcur[bslot<K>(st_ >> K)];
+            const bool allowed = !pinned || ((st_ & (G::SP - 1)) == ov);
+            best = kmin(best, key_of((uint32_t)st_, allowed ? cost : __builtin_inff()));
+        }
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) best = kmin_xor(best, m);
+        if ((tid & 63) == 0) red[tid >> 6] = best;
+        __syncthreads();
+        if (tid == 0) {
+            double b = red[0];
+#pragma unroll
+            for (int wv = 1; wv < kFwdThreads / 64; ++wv) b = kmin(b, red[wv]);
+            // pinned: an all-+inf allowed group leaves the minimum at +inf and
+            // the reference's argmin returns state 0
+            send[tt] = (pinned && key_cost(b) == __builtin_inff()) ? 0 : (int)key_lo(b);
+        }
+        __syncthreads();
+    }
+}
+
+template <int K, int T>
+__global__ __launch_bounds__(kFwdThreads) void fwd_defer_kernel(
+    const float* __restrict__ X, int xstride, int xlen, int nseq,
+    const uint16_t* __restrict__ lut16, int roll, int nsteps, int store_lo,
+    const int32_t* __restrict__ ov_in, float* __restrict__ bm, int32_t* __restrict__ send,
+    uint32_t* __restrict__ err) {
+    __shared__ FwdSmem<K, T> sm;
+    const int q0 = blockIdx.x * T;
+    const int ntile = (nseq - q0) < T ? (nseq - q0) : T;
+    const bool pinned = (ov_in != nullptr);
+    if (threadIdx.x < T)
+        sm.ovs[threadIdx.x] = (pinned && (int)threadIdx.x < ntile) ? ov_in[q0 + threadIdx.x] : -1;
+    fwd_run_defer<K, T>(sm, X, xstride, xlen, q0, ntile, lut16, roll, nsteps, store_lo, pinned,
+                        bm, send + q0, err, (int)threadIdx.x);
+}
+
+// Traceback of the deferred-argmin forward, one lane per sequence: from
+// s = send[q] (the state at step nsteps-1) down to step `stop`; at link i
+// the group j = s_i >> K's NC candidates s' = j + w SP cost
+// fl(fl(fl(f[s'] - x_{i-1})^2) + b_{i-1}[(j >> K) + w Q]) with b_{i-1} from
+// row i-1 of bm (or the start mask when i-1 = 0: 0, or 0 / +inf around the
+// pin ov_in[q]); s_{i-1} = j + w* SP for the first w of the minimum.
+// Targets x_t of step t are X[q][(t - roll) mod xlen].  Outputs as
+// tb_lane_kernel.
+constexpr int kTbDeferChunk = 16;     // candidates recomputed per batch of loads
+
+template <int K>
+__global__ __launch_bounds__(kTbLaneSeqs) void tb_defer_kernel(
+    const float* __restrict__ bm, const float* __restrict__ X, int xstride, int xlen, int roll,
+    const uint16_t* __restrict__ lut16, int nseq, const int32_t* __restrict__ send,
+    const int32_t* __restrict__ ov_in, int nsteps, int stop, int shift,
+    int32_t* __restrict__ sout, int32_t* __restrict__ states, int16_t* __restrict__ trellis) {
+    using G = Geom<K>;
+    constexpr int ROW = kSteps + 2;
+    constexpr int CH = G::NC < kTbDeferChunk ? G::NC : kTbDeferChunk;
+    __shared__ uint16_t st[kTbLaneSeqs][ROW];
+    const int l = threadIdx.x;
+    const int q0 = blockIdx.x * kTbLaneSeqs;
+    const int q = q0 + l;
+    const bool keep = (states != nullptr) || (trellis != nullptr);
+    if (q < nseq) {
+        int s = send[q] & 0xFFFF;
+        if (keep) st[l][nsteps - 1] = (uint16_t)s;
+        const float* xq = X + (size_t)q * xstride;
+        const float* bq = bm + (size_t)q * kSlots * G::SP;
+        const int ov = ov_in ? ov_in[q] : -1;
+        for (int i = nsteps - 1; i > stop; --i) {
+            const int j = (s >> K) & (G::SP - 1);
+            const int a = j >> K;
+            const int u = (i - 1 - roll < 0) ? i - 1 - roll + xlen : i - 1 - roll;
+            const float negx = -xq[u];
+            const float* brow = bq + (size_t)(i - 1) * G::SP + a;
+            float best = 0.0f;
+            int bw = 0;
+#pragma unroll 1
+            for (int w0 = 0; w0 < G::NC; w0 += CH) {
+                float bv[CH], f[CH];
+#pragma unroll
+                for (int w = 0; w < CH; ++w) {
+                    const int g = a + (w0 + w) * G::Q;
+                    bv[w] = (i - 1 == 0) ? ((ov < 0 || g == ov) ? 0.0f : __builtin_inff())
+                                         : brow[(w0 + w) * G::Q];
+                    f[w] = (float)__builtin_bit_cast(_Float16, lut16[j + (w0 + w) * G::SP]);
+                }
+#pragma unroll
+                for (int w = 0; w < CH; ++w) {
+                    const float d = f[w] + negx;
+                    const float c = d * d + bv[w];
+                    if ((w0 == 0 && w == 0) || c < best) {
+                        best = c;
+                        bw = w0 + w;
+                    }
+                }
+            }
+            s = j + bw * G::SP;
+            if (keep) st[l][i - 1] = (uint16_t)s;
+        }
+        if (sout) sout[q] = s >> shift;
+    }
+    __syncthreads();
+    const int nt = (nseq - q0) < kTbLaneSeqs ? (nseq - q0) : kTbLaneSeqs;
+    if (states) {
+        for (int t = 0; t < nt; ++t)
+            for (int e = l; e < nsteps; e += kTbLaneSeqs)
+                states[(size_t)(q0 + t) * nsteps + e] = st[t][e];
+    }
+    if (trellis && nsteps == kSteps) {
+        for (int idx = l; idx < nt * 8 * K; idx += kTbLaneSeqs) {
+            const int t = idx / (8 * K), wd = idx - t * (8 * K);
+            store_word(trellis + (size_t)(q0 + t) * 16 * K + 2 * wd, pack_word<K>(st[t], wd));
+        }
+    }
+}
+
 // ------------------------------------------------------ fused tail-bite
 // Both QTIP passes of n sequences in one launch of 2n single-sequence
 // workgroups, for batches too small to fill the GPU twice over (the 16-row
@@ -1219,6 +1563,73 @@ struct GroupSel {
 };
 
 template <int K>
+struct FwdDeferL {
+    static hipError_t run(const float* X, int xstride, int xlen, int nseq,
+                          const uint16_t* lut16, int roll, int nsteps, int store_lo,
+                          const int32_t* ov_in, void* bm, int32_t* send, uint32_t* err,
+                          int group, hipStream_t s) {
+        if constexpr (K < 4) {
+            return hipErrorInvalidValue;
+        } else {
+            const int T = group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 ? 4 : 8;
+            if (T > max_group<K>()) return hipErrorInvalidValue;
+            const int nwg = (nseq + T - 1) / T;
+            float* b = (float*)bm;
+            if (T == 1)
+                hipLaunchKernelGGL((fwd_defer_kernel<K, 1>), dim3(nwg), dim3(kFwdThreads), 0, s,
+                                   X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo, ov_in,
+                                   b, send, err);
+            else if (T == 2)
+                hipLaunchKernelGGL((fwd_defer_kernel<K, 2>), dim3(nwg), dim3(kFwdThreads), 0, s,
+                                   X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo, ov_in,
+                                   b, send, err);
+            else if constexpr (max_group<K>() >= 4) {
+                if (T == 4)
+                    hipLaunchKernelGGL((fwd_defer_kernel<K, 4>), dim3(nwg), dim3(kFwdThreads),
+                                       0, s, X, xstride, xlen, nseq, lut16, roll, nsteps,
+                                       store_lo, ov_in, b, send, err);
+                else if constexpr (max_group<K>() >= 8)
+                    hipLaunchKernelGGL((fwd_defer_kernel<K, 8>), dim3(nwg), dim3(kFwdThreads),
+                                       0, s, X, xstride, xlen, nseq, lut16, roll, nsteps,
+                                       store_lo, ov_in, b, send, err);
+            }
+            return hipGetLastError();
+        }
+    }
+};
+
+template <int K>
+struct TbDeferL {
+    static hipError_t run(const void* bm, const float* X, int xstride, int xlen, int roll,
+                          const uint16_t* lut16, int nseq, const int32_t* send,
+                          const int32_t* ov_in, int nsteps, int stop, int shift, int32_t* sout,
+                          int32_t* states, int16_t* trellis, hipStream_t s) {
+        if constexpr (K < 4) {
+            return hipErrorInvalidValue;
+        } else {
+            hipLaunchKernelGGL(tb_defer_kernel<K>, dim3((nseq + kTbLaneSeqs - 1) / kTbLaneSeqs),
+                               dim3(kTbLaneSeqs), 0, s, (const float*)bm, X, xstride, xlen, roll,
+                               lut16, nseq, send, ov_in, nsteps, stop, shift, sout, states,
+                               trellis);
+            return hipGetLastError();
+        }
+    }
+};
+
+template <int K>
+struct DeferBytes {
+    static hipError_t run(size_t* out) {
+        if constexpr (K < 4) {
+            *out = 0;
+            return hipErrorInvalidValue;
+        } else {
+            *out = defer_tile_bytes<K>();
+            return hipSuccess;
+        }
+    }
+};
+
+template <int K>
 struct FusedL {
     static hipError_t run(const float* X, int nseq, const uint16_t* lut16, int pivot, int n1,
                           void* bp, int32_t* send, int32_t* ovbuf, uint32_t* flags,
@@ -1394,6 +1805,38 @@ hipError_t launch_unpack(int K, const int16_t* trellis, int nt, int32_t* states,
                          hipStream_t stream) {
     if (nt <= 0) return hipSuccess;
     return dispatch_k<UnpackL>(K, trellis, nt, states, stream);
+}
+
+size_t defer_tile_bytes(int K) {
+    size_t b = 0;
+    if (dispatch_k<DeferBytes>(K, &b) != hipSuccess) return 0;
+    return b;
+}
+
+hipError_t launch_forward_defer(int K, const float* X, int xstride, int xlen, int nseq,
+                                const uint16_t* lut16, int roll, int nsteps, int store_lo,
+                                const int32_t* ov_in, void* bm, int32_t* send, uint32_t* err,
+                                int group, hipStream_t stream) {
+    if (nseq <= 0) return hipSuccess;
+    if (xlen < 1 || xlen > kSteps || nsteps < 1 || nsteps > kSteps || roll < 0 ||
+        roll >= xlen || (roll != 0 && xlen != kSteps) || (roll == 0 && nsteps > xlen) ||
+        store_lo < 0)
+        return hipErrorInvalidValue;
+    return dispatch_k<FwdDeferL>(K, X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo,
+                                 ov_in, bm, send, err, group, stream);
+}
+
+hipError_t launch_traceback_defer(int K, const void* bm, const float* X, int xstride, int xlen,
+                                  int roll, const uint16_t* lut16, int nseq,
+                                  const int32_t* send, const int32_t* ov_in, int nsteps,
+                                  int stop, int shift, int32_t* sout, int32_t* states,
+                                  int16_t* trellis, hipStream_t stream) {
+    if (nseq <= 0) return hipSuccess;
+    if (nsteps < 1 || nsteps > kSteps || stop < 0 || stop >= nsteps || roll < 0 ||
+        roll >= xlen || xlen < 1 || xlen > kSteps)
+        return hipErrorInvalidValue;
+    return dispatch_k<TbDeferL>(K, bm, X, xstride, xlen, roll, lut16, nseq, send, ov_in,
+                                nsteps, stop, shift, sout, states, trellis, stream);
 }
 
 hipError_t launch_fill_u32(uint32_t* p, uint32_t n, uint32_t v, hipStream_t stream) {

@@ -63,6 +63,8 @@ def lib():
         L.xtq_vit_get_lut.argtypes = [cp, vp]
         L.xtq_vit_scratch_per_seq.argtypes = [i32]
         L.xtq_vit_scratch_per_seq.restype = i64
+        L.xtq_vit_chunk_seqs.argtypes = [i32, i32, ctypes.POINTER(ctypes.c_int)]
+        L.xtq_vit_chunk_seqs.restype = i32
         L.xtq_vit_prof_enable.argtypes = [i32]
         L.xtq_vit_prof_enable.restype = i32
         dp = ctypes.POINTER(ctypes.c_double)
@@ -281,6 +283,17 @@ def get_lut(code: str = "mul1") -> torch.Tensor:
 
 def scratch_per_seq(K: int) -> int:
     return int(lib().xtq_vit_scratch_per_seq(int(K)))
+
+
+def chunk_seqs(nseq: int, K: int):
+    """(sequences per scratch chunk, deferred-argmin encode?) the library
+    would use for a tail-bite of nseq sequences at K on the current device
+    (xtq_vit_chunk_seqs)."""
+    d = ctypes.c_int()
+    n = lib().xtq_vit_chunk_seqs(int(nseq), int(K), ctypes.byref(d))
+    if n < 0:
+        raise HipViterbiError("xtq_vit_chunk_seqs", -n)
+    return n, bool(d.value)
 
 
 def prof_enable(on: bool = True):

@@ -40,17 +40,22 @@ def g(s: int) -> torch.Generator:
 
 def ar1_gram(d: int, n_s: int, rho: float, seed: int, device="cpu") -> torch.Tensor:
     """H = X^T X / n_s for n_s AR(1)-correlated samples of dimension d (fp32).
-    Z is drawn on the CPU (reproducible anywhere); the recursion and the Gram
-    product run on `device` in fp64."""
+    Z is drawn and the recursion run on the CPU in fp64 (one rounded multiply,
+    multiply and add per element, as on any device: reproducible anywhere,
+    and no per-channel device launches); the Gram product runs on `device`."""
     Z = torch.randn(n_s, d, generator=g(seed + 100), dtype=torch.float64)
-    Zt = Z.t().contiguous().to(device)                      # rows = channels
+    Zt = Z.t().contiguous()                                 # rows = channels
     del Z
     Xt = torch.empty_like(Zt)
     Xt[0] = Zt[0]
     c = math.sqrt(1.0 - rho * rho)
+    a, b = torch.empty_like(Zt[0]), torch.empty_like(Zt[0])
     for i in range(1, d):
-        Xt[i] = rho * Xt[i - 1] + c * Zt[i]
-    del Zt
+        torch.mul(Xt[i - 1], rho, out=a)
+        torch.mul(Zt[i], c, out=b)
+        torch.add(a, b, out=Xt[i])
+    del Zt, a, b
+    Xt = Xt.to(device)
     H = (Xt @ Xt.t()) / n_s
     return H.float()
 

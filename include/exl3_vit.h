@@ -48,6 +48,11 @@
  *                    64 GiB; no reference counterpart)
  *   XTQ_VIT_SCRATCH  backpointer scratch budget in bytes; larger batches are
  *                    processed in chunks (default 8 GiB)
+ *   XTQ_VIT_DEFER    0: never, 1: always (K >= 4) run the deferred-argmin
+ *                    encode; default: K >= 4 and batches of >= 8192 sequences
+ *   XTQ_VIT_DEFER_SCRATCH  scratch budget of the deferred-argmin encode's
+ *                    minima rows (default 48 GiB, at most half of the free
+ *                    device memory)
  *   XTQ_VIT_GROUP    force 1, 2, 4 or 8 sequences per forward workgroup
  *                    (testing; default chosen from the batch size)
  *   XTQ_VIT_TB_LANES smallest batch whose tracebacks run one lane per sequence
@@ -238,6 +243,17 @@ XTQ_API int xtq_vit_get_lut(const char* code, float* out);
 
 /* Backpointer scratch bytes per sequence for K (sizing information). */
 XTQ_API int64_t xtq_vit_scratch_per_seq(int K);
+
+/*
+ * Sizing information (no reference counterpart): the sequences per scratch
+ * chunk a tail-bite of nseq sequences at K would run in on the current
+ * device with the current environment, and in *deferred (nullable) 1 when
+ * it would take the deferred-argmin encode (group minima rows in HBM, the
+ * argmin recomputed by the traceback; K >= 4 and nseq >= 8192 by default,
+ * XTQ_VIT_DEFER=0/1 to force), else 0.  Returns minus a status code on
+ * error.  Sets the device up like any other entry point.
+ */
+XTQ_API int xtq_vit_chunk_seqs(int nseq, int K, int* deferred);
 
 /*
  * Kernel timing for benchmarks (no reference counterpart; the reference

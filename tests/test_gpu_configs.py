@@ -173,23 +173,13 @@ def test_c5_full_size(xq, hb, c5, oracle_mod, K):
     _run_config(xq, hb, oracle_mod, [c5["W"]], c5["H"], K, False, 8, f"c5 K={K}")
 
 
-def _chunk_rows(hb, K: int, nseq: int, budget: int = 8 << 30) -> int:
-    """Sequences per scratch chunk for the default XTQ_VIT_SCRATCH budget:
-    budget // per-sequence bytes, rounded down to a multiple of 4 x #CU."""
-    per = hb.scratch_per_seq(K)
-    rnd = 4 * torch.cuda.get_device_properties(0).multi_processor_count
-    ch = max(1, budget // per)
-    if ch > rnd:
-        ch -= ch % rnd
-    return min(ch, nseq)
-
-
 def test_headline_batch_every_chunk(hb, wl, oracle_mod):
     """The benchmark's 348,160 independent K=4 tiles in one call: every tile's
     wrap invariant and pack round trip; the first and last 64 tiles of every
     scratch chunk (the chunk loop's offsets into targets, states and trellis,
     and the partial last chunk) and 4,096 random tiles against the oracle."""
-    monkey = os.environ.pop("XTQ_VIT_SCRATCH", None)
+    saved = {v: os.environ.pop(v, None) for v in ("XTQ_VIT_SCRATCH", "XTQ_VIT_DEFER",
+                                                   "XTQ_VIT_DEFER_SCRATCH")}
     try:
         print("case headline 348160 tiles K=4 pivot 128 margin 0", flush=True)
         X = wl.c5_tiles("cuda")
@@ -197,9 +187,10 @@ def test_headline_batch_every_chunk(hb, wl, oracle_mod):
         assert n == 348160
         _, tr = hb.tailbite(X, 4, 128, 0, states=False, trellis=True)
         st = _every_tile(hb, tr, 4)
-        ch = _chunk_rows(hb, 4, n)
+        ch, deferred = hb.chunk_seqs(n, 4)
         starts = list(range(0, n, ch))
-        print(f"{len(starts)} chunks of {ch} (last {n - starts[-1]})", flush=True)
+        print(f"{len(starts)} chunks of {ch} (last {n - starts[-1]}), deferred argmin "
+              f"{deferred}", flush=True)
         assert len(starts) >= 3 and n - starts[-1] < ch
         idx = set()
         for c0 in starts:
@@ -218,5 +209,6 @@ def test_headline_batch_every_chunk(hb, wl, oracle_mod):
         print(f"headline: {idx.size} tiles exact vs oracle, every tile wrap/round trip",
               flush=True)
     finally:
-        if monkey is not None:
-            os.environ["XTQ_VIT_SCRATCH"] = monkey
+        for v, val in saved.items():
+            if val is not None:
+                os.environ[v] = val

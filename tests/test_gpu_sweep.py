@@ -37,7 +37,12 @@ def _targets(rng, lut, n, kind):
 
 
 @pytest.mark.parametrize("K", range(2, 8))
-def test_tailbite_sweep(hb, oracle_mod, mul1_lut, K):
+@pytest.mark.parametrize("defer", ("0", "1"))
+def test_tailbite_sweep(hb, oracle_mod, mul1_lut, K, defer, monkeypatch):
+    """defer "1": the deferred-argmin encode (K >= 4) on the same sweep."""
+    if defer == "1" and K < 4:
+        pytest.skip("the deferred-argmin encode runs K >= 4")
+    monkeypatch.setenv("XTQ_VIT_DEFER", defer)
     rng = np.random.default_rng(9000 + K)
     n, bad = 64, []
     for kind in ("gauss", "codebook", "grid", "student", "codebook0", "tiny"):

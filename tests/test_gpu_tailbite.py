@@ -85,24 +85,30 @@ def test_short_runs_vs_oracle(hb, oracle_mod, mul1_lut, K):
 
 
 @pytest.mark.parametrize("K", range(2, 8))
-@pytest.mark.parametrize("group", ["1", "2", "4", "8", "fused"])
+@pytest.mark.parametrize("group", ["1", "2", "4", "8", "fused", "d1", "d2", "d4", "d8"])
 def test_oracle_random(hb, oracle_mod, mul1_lut, K, group, monkeypatch):
     """Random Gaussian and tie-heavy batches against the oracle, with each
     code path forced: separate pass launches at 1, 2, 4 or 8 sequences per
-    workgroup, or the fused two-pass launch; odd batch sizes included."""
+    workgroup, the fused two-pass launch, or (K >= 4, "d*") the
+    deferred-argmin forward and its recomputing traceback at 1, 2, 4 or 8
+    sequences per workgroup; odd batch sizes included."""
+    if group.startswith("d") and K < 4:
+        pytest.skip("the deferred-argmin encode runs K >= 4")
+    monkeypatch.setenv("XTQ_VIT_DEFER", "1" if group.startswith("d") else "0")
     if group == "fused":
         monkeypatch.setenv("XTQ_VIT_FUSED", "1")
     else:
         monkeypatch.setenv("XTQ_VIT_FUSED", "0")
-        monkeypatch.setenv("XTQ_VIT_GROUP", group)
-    rng = np.random.default_rng(1000 * K + (9 if group == "fused" else int(group)))
+        monkeypatch.setenv("XTQ_VIT_GROUP", group.lstrip("d"))
+    rng = np.random.default_rng(1000 * K + (9 if group == "fused" else int(group.lstrip("d"))))
     n = 7
     X = rng.standard_normal((n, 256)).astype(np.float32)
     X[1] = mul1_lut[rng.integers(0, 65536, 256)]          # exact codebook values
     X[2] = 0.0                                             # all ties at step 0
     X[3] *= 40.0                                           # large costs
     X[4] = np.round(X[4] * 2) / 2                          # coarse grid
-    for pivot, margin in ((128, 0), (3, 16), (250, 16), (200, 100)):
+    for pivot, margin in ((128, 0), (3, 16), (250, 16), (200, 100), (0, 0), (0, 1),
+                          (255, 0)):
         print(f"case K={K} group={group} pivot={pivot} margin={margin}", flush=True)
         want = oracle_mod.tailbite(X, mul1_lut, K, 16, pivot=pivot, margin=margin)
         got, tr = _run(hb, X, K, pivot, margin, trellis=True)
@@ -171,6 +177,38 @@ def test_batch_position_invariance(hb, K):
     assert ((st_all[:, 0] >> K) == (st_all[:, -1] & (SP - 1))).all()
 
 
+@pytest.mark.parametrize("K", (4, 5, 6, 7))
+def test_deferred_chunks(hb, oracle_mod, mul1_lut, K, monkeypatch):
+    """The deferred-argmin encode over a batch split into three chunks (a
+    small XTQ_VIT_DEFER_SCRATCH) with a partial last one equals the
+    key-argmin encode of the same batch, and each chunk's first and last 16
+    tiles equal the oracle (tie-heavy rows included)."""
+    rng = np.random.default_rng(60 + K)
+    n = 2 * 1024 + 300
+    X = rng.standard_normal((n, 256)).astype(np.float32)
+    X[::97] = mul1_lut[rng.integers(0, 65536, (len(X[::97]), 256))]
+    X[5::211] = 0.0
+    Xd = torch.from_numpy(X).cuda()
+    monkeypatch.setenv("XTQ_VIT_DEFER", "0")
+    print(f"case K={K} n={n} key argmin", flush=True)
+    ref, ref_tr = hb.tailbite(Xd, K, 147, 16, trellis=True)
+    monkeypatch.setenv("XTQ_VIT_DEFER", "1")
+    per = hb.scratch_per_seq(K)       # backpointer bytes; the minima rows are larger
+    monkeypatch.setenv("XTQ_VIT_DEFER_SCRATCH", str(1024 * 255 * (1 << (16 - K)) * 4 + 4096))
+    ch, deferred = hb.chunk_seqs(n, K)
+    assert deferred and per > 0
+    print(f"case K={K} n={n} deferred argmin, chunks of {ch}", flush=True)
+    got, tr = hb.tailbite(Xd, K, 147, 16, trellis=True)
+    starts = list(range(0, n, ch))
+    assert len(starts) >= 3 and n - starts[-1] < ch
+    assert torch.equal(got, ref) and torch.equal(tr, ref_tr)
+    idx = sorted({i for c0 in starts for i in list(range(c0, c0 + 16)) +
+                  list(range(min(n, c0 + ch) - 16, min(n, c0 + ch)))})
+    want = oracle_mod.tailbite(X[idx], mul1_lut, K, 16, pivot=147, margin=16,
+                               nthreads=len(os.sched_getaffinity(0)))
+    np.testing.assert_array_equal(got[idx].cpu().numpy(), want)
+
+
 @pytest.mark.parametrize("K", (2, 4, 7))
 def test_forced_chunks(hb, oracle_mod, mul1_lut, K, monkeypatch):
     """XTQ_VIT_SCRATCH is read on every call: a budget of 2048 sequences
@@ -185,6 +223,7 @@ def test_forced_chunks(hb, oracle_mod, mul1_lut, K, monkeypatch):
     rng = np.random.default_rng(40 + K)
     X = torch.from_numpy(rng.standard_normal((n, 256)).astype(np.float32)).cuda()
     monkeypatch.delenv("XTQ_VIT_SCRATCH", raising=False)
+    monkeypatch.setenv("XTQ_VIT_DEFER", "0")
     print(f"case K={K} n={n} unchunked", flush=True)
     ref, ref_tr = hb.tailbite(X, K, 147, 16, trellis=True)
     monkeypatch.setenv("XTQ_VIT_SCRATCH", str(2048 * per))
