@@ -120,9 +120,16 @@ def cpu_baseline(X: torch.Tensor, trellis: torch.Tensor, budget_s: float = 12.0)
                      .all(axis=1).sum())
         done += len(idx)
     port_tps = done / t_cpu
-    # wider check through the C oracle (multi-threaded, not timed)
+    # wider check through the C oracle (multi-threaded, not timed): 2,048
+    # further random tiles and the first and last 16 tiles of every scratch
+    # chunk the library processed the batch in
     O.build()
-    idx = torch.from_numpy(order[done:done + 1024]).to(X.device)
+    ch, _ = hb.chunk_seqs(n, KBITS)
+    edges = {i for c0 in range(0, n, ch)
+             for i in list(range(c0, min(n, c0 + 16))) + list(range(max(c0, min(n, c0 + ch) - 16),
+                                                                 min(n, c0 + ch)))}
+    sel = sorted((set(order[done:done + 2048].tolist()) | edges) - set(order[:done].tolist()))
+    idx = torch.tensor(sel, dtype=torch.long, device=X.device)
     want = O.tailbite(X[idx].cpu().numpy(), lut.numpy(), KBITS, 16, pivot=PIVOT,
                       margin=MARGIN, nthreads=cores)
     exact2 = int((want == gpu_states[idx].cpu().numpy()).all(axis=1).sum())
@@ -130,7 +137,10 @@ def cpu_baseline(X: torch.Tensor, trellis: torch.Tensor, budget_s: float = 12.0)
              "cpu": _cpu_model(),
              "sample": f"{done} tiles drawn uniformly from the 348,160-tile K=4 workload, "
                        f"torch-CPU restatement of quantize_seq_tailbite, {cores} threads"},
-            {"tiles_checked": done + len(idx), "tiles_exact": exact + exact2})
+            {"tiles_checked": done + len(idx), "tiles_exact": exact + exact2,
+             "oracle_sample": f"{len(idx)} tiles through the C oracle: 2,048 random and the "
+                              f"first/last 16 of each of the {(n + ch - 1) // ch} chunks of "
+                              f"{ch}"})
 
 
 def k_sweep(X: torch.Tensor, n: int = 65536):

@@ -80,6 +80,30 @@ __global__ __launch_bounds__(kThreads) void probe_kernel(float* __restrict__ out
                 for (int c = g0; c < g0 + 8; ++c)
                     asm volatile("v_min_f64 %0, %0, %1" : "+v"(d[c]) : "v"((double)b));
             }
+        } else if constexpr (OP == 9) {               // v_min3_f32 alone
+#pragma unroll
+            for (int c = 0; c < kChains; ++c)
+                asm volatile("v_min3_f32 %0, %0, %1, %1" : "+v"(x[c]) : "v"(b));
+        } else if constexpr (OP == 10) {              // deferred-argmin mix, grouped by 8
+#pragma unroll
+            for (int g0 = 0; g0 < kChains; g0 += 8) {
+#pragma unroll
+                for (int c = g0; c < g0 + 8; ++c)
+                    asm volatile("v_add_f32 %0, %1, %2" : "=v"(x[c]) : "v"(x[c]), "v"(b));
+#pragma unroll
+                for (int c = g0; c < g0 + 8; ++c) asm volatile("v_mul_f32 %0, %0, %0" : "+v"(x[c]));
+#pragma unroll
+                for (int c = g0; c < g0 + 8; ++c)
+                    asm volatile("v_add_f32 %0, %0, %1" : "+v"(x[c]) : "v"(b));
+                // the 8 costs' minimum by a v_min3_f32 tree (4 instructions)
+                asm volatile("v_min3_f32 %0, %0, %1, %2"
+                             : "+v"(x[g0]) : "v"(x[g0 + 1]), "v"(x[g0 + 2]));
+                asm volatile("v_min3_f32 %0, %0, %1, %2"
+                             : "+v"(x[g0 + 3]) : "v"(x[g0 + 4]), "v"(x[g0 + 5]));
+                asm volatile("v_min3_f32 %0, %0, %1, %2"
+                             : "+v"(x[g0 + 6]) : "v"(x[g0 + 7]), "v"(x[g0]));
+                asm volatile("v_min_f32 %0, %0, %1" : "+v"(x[g0 + 6]) : "v"(x[g0 + 3]));
+            }
         } else if constexpr (OP == 5) {               // candidate mix, dependency order
 #pragma unroll
             for (int c = 0; c < kChains; ++c) {
@@ -114,7 +138,7 @@ __global__ __launch_bounds__(kThreads) void probe_kernel(float* __restrict__ out
 }
 
 // VALU instructions per chain per iteration of each probe.
-constexpr int kOpsPerChain[9] = {1, 1, 1, 1, 1, 4, 4, 4, 4};
+constexpr double kOpsPerChain[11] = {1, 1, 1, 1, 1, 4, 4, 4, 4, 1, 3.5};
 
 template <int OP>
 hipError_t launch(int nwg, float* out, hipStream_t s) {
@@ -132,7 +156,9 @@ hipError_t launch_any(int which, int nwg, float* out, hipStream_t s) {
         case 5: return launch<5>(nwg, out, s);
         case 6: return launch<6>(nwg, out, s);
         case 7: return launch<7>(nwg, out, s);
-        default: return launch<8>(nwg, out, s);
+        case 8: return launch<8>(nwg, out, s);
+        case 9: return launch<9>(nwg, out, s);
+        default: return launch<10>(nwg, out, s);
     }
 }
 
@@ -141,13 +167,15 @@ hipError_t launch_any(int which, int nwg, float* out, hipStream_t s) {
 // Times probe `which` (0 v_mul_f32, 1 v_add_f32, 2 v_fma_f32, 3 v_fma_mix_f32,
 // 4 v_min_f64, 5/6 the candidate mix with a packed fp16 codebook in
 // dependency order / grouped by opcode, 7/8 the mix with an fp32 codebook in
-// dependency order / grouped by opcode) on every CU of the current device
+// dependency order / grouped by opcode, 9 v_min3_f32, 10 the deferred-argmin
+// mix: add, mul, add per candidate and a v_min3_f32 tree over 8 -- 3.5
+// instructions per candidate) on every CU of the current device
 // and returns its VALU lane-instructions per second.  Status: 0 ok, 1 no
 // device, 2 allocation failed, 4 HIP error, 8 unknown probe, 12 null output.
 extern "C" __attribute__((visibility("default"))) int xtq_valu_probe(int which,
                                                                      double* lane_ops_per_s) {
     if (!lane_ops_per_s) return 12;
-    if (which < 0 || which > 8) return 8;
+    if (which < 0 || which > 10) return 8;
     int dev = 0, ncu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
