@@ -5,6 +5,7 @@ Run once, in the build container only (the reference tree is not present on
 the GPU host):
 
     python tests/golden/make_golden.py /root/reference/quantize
+    python tests/golden/make_golden.py /root/reference/quantize --ties
 
 It imports the reference quantizer module (quantize/quantize.py) on CPU and
 records input/output vectors for the functions that closed forms, invariants
@@ -18,6 +19,9 @@ and brute force cannot pin:
     channel_scales off and on                            (quantize.py:750-875)
   * quantize() harness with a U factor, margin 16        (quantize.py:894-966)
   * prepare_incoherence                                  (quantize.py:969-1058)
+--ties writes ties.npz alone: quantize_seq_tailbite on 24 sequences per K
+whose results hinge on exact cost ties (six kinds, tie_forcing_inputs) at four
+pivot/margin pairs, and viterbi() pinned and back_from runs on them.
 Only data (inputs and expected outputs) is written, as compressed .npz files
 loadable with numpy.load(allow_pickle=False).
 """
@@ -57,6 +61,60 @@ def tie_heavy_inputs(lut: np.ndarray, rng: np.random.Generator, n: int):
         else:
             X[q] = np.round(rng.standard_normal(256) * 2.0) / 2.0
     return X
+
+
+def tie_forcing_inputs(lut: np.ndarray, rng: np.random.Generator, n: int):
+    """Six kinds of targets, four of each, under which exactly equal path
+    costs decide the result.  Large targets round fl(f - x) and the growing
+    fp32 sums onto a coarse grid, so many candidates tie exactly: N(0, 3000);
+    U(-1e5, 1e5); U(-1e9, 1e9) (fl(f - x) = -x for every state: every
+    candidate ties at every step); exact codebook values with every fourth
+    target U(-1e5, 1e5).  Plus exact codebook values and midpoints of two
+    codebook values (f_a - x = -(f_b - x) exactly, equal emissions)."""
+    X = np.empty((n, 256), dtype=np.float32)
+    vals = np.unique(lut)
+    for q in range(n):
+        kind = q % 6
+        if kind == 0:
+            X[q] = lut[rng.integers(0, lut.size, 256)]
+        elif kind == 1:
+            a = rng.integers(0, vals.size - 1, 256)
+            b = np.minimum(vals.size - 1, a + rng.integers(1, 4, 256))
+            X[q] = (vals[a].astype(np.float64) + vals[b]) / 2.0
+        elif kind == 2:
+            X[q] = rng.standard_normal(256) * 3000.0
+        elif kind == 3:
+            X[q] = rng.uniform(-1e5, 1e5, 256)
+        elif kind == 4:
+            X[q] = rng.uniform(-1e9, 1e9, 256)
+        else:
+            X[q] = lut[rng.integers(0, lut.size, 256)]
+            X[q, ::4] = rng.uniform(-1e5, 1e5, 64)
+    return X
+
+
+def main_ties(refdir: str):
+    sys.path.insert(0, refdir)
+    import quantize as xq  # the reference module, CPU only
+    torch.set_num_threads(8)
+    lut = xq.get_lut("exl3_mul1", 16)
+    lut_np = lut.numpy().astype(np.float32)
+    t0 = time.time()
+    rng = np.random.default_rng(20261202)
+    data = {}
+    for K in range(2, 8):
+        X = tie_forcing_inputs(lut_np, rng, 24)
+        data[f"X_K{K}"] = X
+        Xt = torch.from_numpy(X.T.copy())                # [256, 24]
+        for p, m in ((128, 0), (147, 16), (0, 0), (255, 16)):
+            st = xq.quantize_seq_tailbite(Xt, lut, K, 16, pivot=p, margin=m)
+            data[f"S_K{K}_m{m}_p{p}"] = st.t().numpy().astype(np.int32)
+        ov = torch.from_numpy((np.arange(24) * 1237) % (1 << (16 - K)))
+        data[f"VPov_K{K}"] = ov.numpy().astype(np.int32)
+        data[f"VP_K{K}"] = xq.viterbi(Xt, lut, K, 16, overlap=ov).t().numpy().astype(np.int32)
+        data[f"VB_K{K}"] = xq.viterbi(Xt[:200], lut, K, 16, back_from=60).numpy().astype(np.int32)
+        print(f"  ties K={K} done {time.time() - t0:.1f}s", flush=True)
+    np.savez_compressed(os.path.join(OUT, "ties.npz"), **data)
 
 
 def main(refdir: str):
@@ -157,4 +215,9 @@ def main(refdir: str):
 
 
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference/quantize")
+    args = [a for a in sys.argv[1:] if not a.startswith("--")]
+    ref = args[0] if args else "/root/reference/quantize"
+    if "--ties" in sys.argv[1:]:
+        main_ties(ref)
+    else:
+        main(ref)

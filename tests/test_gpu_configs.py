@@ -18,6 +18,13 @@ states bit for bit against the C oracle on the targets the kernel computed
 (the reference's per-launch dual method, quantize.py:687-717).  The batched
 workload checks the first and last 64 tiles of every scratch chunk the
 library processes, and a random sample, against the oracle.
+
+Every tile, bit for bit: the headline batch, c2, c4 and c5 at K=4 are also
+encoded tile by tile by the reference's own torch Viterbi (the tensor
+operations of quantize.py:218-354, oracle/torch_port.py) run on the GPU, on
+the same targets, and every tile's states must match -- the reference's
+whole-tensor check (check_tensor_bitexact.py:69-123).  The GPU run of that
+port is itself pinned to the C oracle on tie-heavy tiles for every K first.
 """
 import os
 
@@ -82,6 +89,47 @@ def _oracle_rows(O, lut, xt: torch.Tensor, st: torch.Tensor, rows, K: int, label
     return checked
 
 
+PORT_BATCH = 16384          # tiles per torch-port launch (4 GiB of fp32 costs)
+
+
+def _every_tile_vs_port(lutd, X: torch.Tensor, st: torch.Tensor, K: int, label: str,
+                        pivot: int = 128, margin: int = 0) -> int:
+    """States st [n, 256] of targets X [n, 256] (both on the GPU) against the
+    reference's torch tail-bite run on the GPU, every tile."""
+    from oracle import torch_port as TP
+    n = X.shape[0]
+    bad = 0
+    for c0 in range(0, n, PORT_BATCH):
+        c1 = min(n, c0 + PORT_BATCH)
+        want = TP.tailbite(X[c0:c1].t().contiguous(), lutd, K, 16, pivot=pivot, margin=margin)
+        bad += int((want.t() != st[c0:c1].long()).any(dim=1).sum())
+    assert bad == 0, f"{label}: {bad} of {n} tiles differ from the reference's torch Viterbi"
+    print(f"{label}: every tile ({n}) exact vs the reference's torch Viterbi on the GPU",
+          flush=True)
+    return n
+
+
+def test_torch_port_on_gpu_vs_oracle(oracle_mod):
+    """The torch port run on the GPU (the every-tile checker below) against the
+    C oracle: Gaussian, exact-codebook (tie-heavy) and all-zero targets, every K,
+    the default and the reference harness's pivot/margin."""
+    lut = oracle_mod.code_lut("exl3_mul1")
+    lutd = torch.from_numpy(lut).cuda()
+    from oracle import torch_port as TP
+    rng = np.random.default_rng(11)
+    X = rng.standard_normal((192, 256)).astype(np.float32)
+    X[:64] = lut[rng.integers(0, 65536, (64, 256))]
+    X[64:80] = 0.0
+    X[80:96] = np.round(X[80:96] * 4) / 4
+    for K in range(2, 8):
+        for pivot, margin in ((128, 0), (147, 16)):
+            want = oracle_mod.tailbite(X, lut, K, 16, pivot=pivot, margin=margin,
+                                       nthreads=NTHREADS)
+            got = TP.tailbite(torch.from_numpy(X.T.copy()).cuda(), lutd, K, 16, pivot=pivot,
+                              margin=margin).t().cpu().numpy()
+            assert np.array_equal(got, want), f"torch port on the GPU != oracle (K={K}, p={pivot})"
+
+
 def _reconstruct(xq, hb, r, K: int, cs: bool) -> torch.Tensor:
     """W_hat [out, in] from the member's trellis alone, on the GPU, with
     quantize_linear's own transform (quantize.py:862-866)."""
@@ -97,9 +145,10 @@ def _reconstruct(xq, hb, r, K: int, cs: bool) -> torch.Tensor:
     return W_hat.t().contiguous()
 
 
-def _run_config(xq, hb, O, Ws, H, Ks, cs, rows_per_run, label):
+def _run_config(xq, hb, O, Ws, H, Ks, cs, rows_per_run, label, every_tile=False):
     """quantize_linear_group on the GPU with the kernel's targets kept; every
-    tile checked, sampled block rows against the oracle."""
+    tile checked, sampled block rows against the oracle (and, with
+    every_tile, every tile against the reference's torch Viterbi)."""
     lut = O.code_lut("exl3_mul1")
     dev = torch.device("cuda")
     Ws = [W.float().to(dev) for W in Ws]
@@ -123,6 +172,10 @@ def _run_config(xq, hb, O, Ws, H, Ks, cs, rows_per_run, label):
         total += st.shape[0] * st.shape[1]
         checked += _oracle_rows(O, lut, xt[:, c0 // 16:(c0 + nc) // 16], st,
                                 _sample_rows(tk, rows_per_run), K, f"{label} K={K}")
+        if every_tile:
+            _every_tile_vs_port(torch.from_numpy(lut).to(dev),
+                                xt[:, c0 // 16:(c0 + nc) // 16].reshape(-1, 256),
+                                st.reshape(-1, 256), K, f"{label} K={K}")
     Kl = [Ks] * len(Ws) if isinstance(Ks, int) else list(Ks)
     for W, r, K in zip(Ws, rs, Kl):
         assert r["trellis"].shape == (W.shape[1] // 16, W.shape[0] // 16, 16 * K)
@@ -136,7 +189,7 @@ def _run_config(xq, hb, O, Ws, H, Ks, cs, rows_per_run, label):
 def test_c2_full_size(xq, hb, wl, oracle_mod):
     print("case c2 4096x4096 K=4", flush=True)
     w = wl.c2(device="cuda")
-    _run_config(xq, hb, oracle_mod, [w["W"]], w["H"], 4, False, 16, "c2")
+    _run_config(xq, hb, oracle_mod, [w["W"]], w["H"], 4, False, 16, "c2", every_tile=True)
 
 
 @pytest.fixture(scope="module")
@@ -157,7 +210,7 @@ def test_c4_full_size(xq, hb, wl, oracle_mod):
     w = wl.c4(device="cuda")
     Ks = [m["K"] for m in w["members"]]
     _run_config(xq, hb, oracle_mod, [m["W"] for m in w["members"]], w["H"], Ks, True, 8,
-                "c4")
+                "c4", every_tile=True)
 
 
 @pytest.fixture(scope="module")
@@ -170,14 +223,16 @@ def c5(wl):
 @pytest.mark.parametrize("K", (6, 4))
 def test_c5_full_size(xq, hb, c5, oracle_mod, K):
     print(f"case c5 5120x17408 K={K}", flush=True)
-    _run_config(xq, hb, oracle_mod, [c5["W"]], c5["H"], K, False, 8, f"c5 K={K}")
+    _run_config(xq, hb, oracle_mod, [c5["W"]], c5["H"], K, False, 8, f"c5 K={K}",
+                every_tile=(K == 4))
 
 
 def test_headline_batch_every_chunk(hb, wl, oracle_mod):
     """The benchmark's 348,160 independent K=4 tiles in one call: every tile's
     wrap invariant and pack round trip; the first and last 64 tiles of every
     scratch chunk (the chunk loop's offsets into targets, states and trellis,
-    and the partial last chunk) and 4,096 random tiles against the oracle."""
+    and the partial last chunk) and 4,096 random tiles against the oracle;
+    every tile against the reference's torch Viterbi run on the GPU."""
     saved = {v: os.environ.pop(v, None) for v in ("XTQ_VIT_SCRATCH", "XTQ_VIT_DEFER",
                                                    "XTQ_VIT_DEFER_SCRATCH")}
     try:
@@ -208,6 +263,7 @@ def test_headline_batch_every_chunk(hb, wl, oracle_mod):
         assert bad.size == 0, f"tiles {bad[:8].tolist()} differ from the oracle"
         print(f"headline: {idx.size} tiles exact vs oracle, every tile wrap/round trip",
               flush=True)
+        _every_tile_vs_port(torch.from_numpy(lut).cuda(), X, st, 4, "headline")
     finally:
         for v, val in saved.items():
             if val is not None:

@@ -49,6 +49,38 @@ def test_golden_tailbite(hb, K):
                 np.testing.assert_array_equal(tr, g[f"P_K{K}"])
 
 
+TIE_CASES = ((128, 0), (147, 16), (0, 0), (255, 16))
+
+
+@pytest.mark.parametrize("group,K", [(g, K) for g in ("auto", "1", "2", "4", "8", "fused")
+                                     for K in range(2, 8)]
+                         + [(g, K) for g in ("d1", "d4", "d8") for K in range(4, 8)])
+def test_golden_ties(hb, K, group, monkeypatch):
+    """The reference's quantize_seq_tailbite and viterbi() on 24 tie-forcing
+    sequences per K (exact codebook values, codebook midpoints, constant
+    runs, a 0.25 grid, sparse values, +-8 beyond the codebook), through every
+    code path: the library's own choice, separate pass launches at 1, 2, 4 or
+    8 sequences per workgroup, the fused launch, the deferred argmin."""
+    if group != "auto":
+        monkeypatch.setenv("XTQ_VIT_DEFER", "1" if group.startswith("d") else "0")
+        monkeypatch.setenv("XTQ_VIT_FUSED", "1" if group == "fused" else "0")
+        if group != "fused":
+            monkeypatch.setenv("XTQ_VIT_GROUP", group.lstrip("d"))
+    g = load_golden("ties.npz")
+    X = g[f"X_K{K}"]
+    for p, m in TIE_CASES:
+        print(f"case ties K={K} group={group} pivot={p} margin={m}", flush=True)
+        st, _ = _run(hb, X, K, p, m)
+        np.testing.assert_array_equal(st, g[f"S_K{K}_m{m}_p{p}"], err_msg=f"K={K} m={m} p={p}")
+    if group == "auto":
+        Xd = torch.from_numpy(X).cuda()
+        ov = torch.from_numpy(g[f"VPov_K{K}"]).cuda()
+        np.testing.assert_array_equal(hb.viterbi(Xd, K, overlap=ov).cpu().numpy(),
+                                      g[f"VP_K{K}"])
+        vb = hb.viterbi(Xd[:, :200].contiguous(), K, back_from=60)
+        np.testing.assert_array_equal(vb.cpu().numpy(), g[f"VB_K{K}"])
+
+
 @pytest.mark.parametrize("K", range(2, 8))
 def test_golden_viterbi_runs(hb, K):
     """Single Viterbi runs equal the reference's viterbi(): free with full
@@ -84,16 +116,16 @@ def test_short_runs_vs_oracle(hb, oracle_mod, mul1_lut, K):
                 got, oracle_mod.viterbi(X, mul1_lut, K, 16, back_from=T // 2))
 
 
-@pytest.mark.parametrize("K", range(2, 8))
-@pytest.mark.parametrize("group", ["1", "2", "4", "8", "fused", "d1", "d2", "d4", "d8"])
+# the deferred-argmin paths ("d*") exist for K >= 4 only
+@pytest.mark.parametrize("group,K", [(g, K) for g in ("1", "2", "4", "8", "fused")
+                                     for K in range(2, 8)]
+                         + [(g, K) for g in ("d1", "d2", "d4", "d8") for K in range(4, 8)])
 def test_oracle_random(hb, oracle_mod, mul1_lut, K, group, monkeypatch):
     """Random Gaussian and tie-heavy batches against the oracle, with each
     code path forced: separate pass launches at 1, 2, 4 or 8 sequences per
     workgroup, the fused two-pass launch, or (K >= 4, "d*") the
     deferred-argmin forward and its recomputing traceback at 1, 2, 4 or 8
     sequences per workgroup; odd batch sizes included."""
-    if group.startswith("d") and K < 4:
-        pytest.skip("the deferred-argmin encode runs K >= 4")
     monkeypatch.setenv("XTQ_VIT_DEFER", "1" if group.startswith("d") else "0")
     if group == "fused":
         monkeypatch.setenv("XTQ_VIT_FUSED", "1")

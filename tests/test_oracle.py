@@ -123,6 +123,70 @@ def test_oracle_vs_reference_golden(oracle_mod, mul1_lut, K):
                                   g[f"D_K{K}"])
 
 
+TIE_CASES = ((128, 0), (147, 16), (0, 0), (255, 16))
+
+
+@pytest.mark.parametrize("K", range(2, 8))
+def test_oracle_vs_reference_ties(oracle_mod, mul1_lut, K):
+    """The reference's outputs on 24 tie-forcing sequences per K (ties.npz):
+    the C oracle and the torch restatement reproduce every state."""
+    import torch
+    from oracle import torch_port
+    g = load_golden("ties.npz")
+    X = g[f"X_K{K}"]
+    for p, m in TIE_CASES:
+        want = g[f"S_K{K}_m{m}_p{p}"]
+        np.testing.assert_array_equal(oracle_mod.tailbite(X, mul1_lut, K, 16, pivot=p, margin=m),
+                                      want, err_msg=f"oracle m={m} p={p}")
+        got = torch_port.tailbite(torch.from_numpy(X.T.copy()), torch.from_numpy(mul1_lut), K,
+                                  16, pivot=p, margin=m).t().numpy()
+        np.testing.assert_array_equal(got, want, err_msg=f"torch port m={m} p={p}")
+    np.testing.assert_array_equal(
+        oracle_mod.viterbi(X, mul1_lut, K, 16, overlap=g[f"VPov_K{K}"]), g[f"VP_K{K}"])
+    np.testing.assert_array_equal(
+        oracle_mod.viterbi(X[:, :200], mul1_lut, K, 16, back_from=60), g[f"VB_K{K}"])
+
+
+@pytest.mark.parametrize("K", (2, 4, 7))
+def test_ties_fixture_pins_the_tie_rule(mul1_lut, K):
+    """A planted 'last index wins' rule (the torch restatement with the
+    candidate order reversed in every min and in the final argmin) changes
+    most tie-forcing sequences of the fixture: the fixture pins the first-index
+    rule at L=16 on its own."""
+    import torch
+    g = load_golden("ties.npz")
+    X = torch.from_numpy(g[f"X_K{K}"].T.copy())
+    lut = torch.from_numpy(mul1_lut)
+    S, NC, SP = 1 << 16, 1 << K, 1 << (16 - K)
+    T, B = X.shape
+
+    def last_index_viterbi(x):
+        def emit(i):
+            return (lut.view(1, S) - x[i].unsqueeze(-1)).square()
+        cost = emit(0)
+        bps = []
+        for i in range(1, T):
+            rev = cost.view(B, NC, SP).flip(1).min(dim=1)
+            bps.append(NC - 1 - rev.indices)
+            e = emit(i)
+            e.view(B, SP, NC).add_(rev.values.unsqueeze(-1))
+            cost = e
+        s = S - 1 - cost.flip(1).argmin(dim=1)
+        st = [s]
+        for i in range(T - 1, 0, -1):
+            j = s >> K
+            s = j + bps[i - 1].gather(1, j.unsqueeze(1)).squeeze(1) * SP
+            st.append(s)
+        return torch.stack(st[::-1]).t().numpy()
+
+    planted = last_index_viterbi(X)
+    from oracle import torch_port
+    want = torch_port.viterbi(X, lut, K, 16).t().numpy()
+    differ = int((planted != want).any(axis=1).sum())
+    print(f"K={K}: the planted rule changes {differ} of {B} sequences")
+    assert differ >= 10, f"only {differ} of {B} sequences separate the tie rules"
+
+
 # ------------------------------------------------------------- brute force
 @pytest.mark.parametrize("L,K,T,seed", [(4, 2, 6, 1), (4, 1, 7, 2), (6, 2, 5, 3),
                                         (6, 3, 4, 4)])
