@@ -684,7 +684,7 @@ struct ChainGroup { int jc0, tnl, K; int16_t* trellis; };
 // backpointer slots and target rows.
 int run_ldlq_chain(DevCtx& cx, const float* W, const float* L, int k, int n,
                    const ChainGroup* grp, int ng, Code code, int margin, int pivot,
-                   float* hatW, int32_t* states, float* targets, hipStream_t s) {
+                   int buf_cols, float* hatW, int32_t* states, float* targets, hipStream_t s) {
     const int tk = k / 16;
     const size_t ntile = (size_t)tk * (size_t)(n / 16);
     int tng[kMaxChainGroups], Kg[kMaxChainGroups], nwg[kMaxChainGroups];
@@ -756,7 +756,7 @@ int run_ldlq_chain(DevCtx& cx, const float* W, const float* L, int k, int n,
             Kg[g], W, L ? cx.Lt : nullptr, k, n, grp[g].jc0, grp[g].tnl, cx.lut16[code], pivot,
             n1, (uint8_t*)cx.bp + bp_off[g], nwg[g], targets ? targets : cx.xbuf + x_off[g] * xtq::kSteps,
             targets ? 1 : 0, hatW, cx.E, states, grp[g].trellis, cx.cflags, cx.ccount + g,
-            cx.epoch, kSpinLimit, cx.err, sg);
+            cx.epoch, kSpinLimit, cx.err, buf_cols, sg);
         if (e == hipSuccess && g &&
             (hipEventRecord(cx.join[g - 1], sg) != hipSuccess ||
              hipStreamWaitEvent(s, cx.join[g - 1], 0) != hipSuccess))
@@ -982,16 +982,16 @@ int xtq_vit_status_dev(void* stream) {
 }
 
 int xtq_ldlq_chain_dev(const float* d_W, const float* d_L, int k, int n, int K,
-                       const char* code, int margin, int pivot, float* d_hatW,
+                       const char* code, int margin, int pivot, int buf_cols, float* d_hatW,
                        int32_t* d_states, int16_t* d_trellis, float* d_targets, void* stream) {
     int16_t* tr[1] = {d_trellis};
-    return xtq_ldlq_chain_multi_dev(d_W, d_L, k, n, 1, &n, &K, code, margin, pivot, d_hatW,
-                                    d_states, tr, d_targets, stream);
+    return xtq_ldlq_chain_multi_dev(d_W, d_L, k, n, 1, &n, &K, code, margin, pivot, buf_cols,
+                                    d_hatW, d_states, tr, d_targets, stream);
 }
 
 int xtq_ldlq_chain_multi_dev(const float* d_W, const float* d_L, int k, int n, int ngroups,
                              const int* h_ncols, const int* h_K, const char* code, int margin,
-                             int pivot, float* d_hatW, int32_t* d_states,
+                             int pivot, int buf_cols, float* d_hatW, int32_t* d_states,
                              int16_t* const* h_trellis, float* d_targets, void* stream) {
     std::lock_guard<std::mutex> lk(g_mu);
     if (!d_W || !d_hatW || !h_ncols || !h_K || !h_trellis) return 12;
@@ -1010,6 +1010,7 @@ int xtq_ldlq_chain_multi_dev(const float* d_W, const float* d_L, int k, int n, i
         col += h_ncols[g];
     }
     if (pivot < 0 || pivot >= xtq::kSteps || margin < 0) return 10;
+    if (buf_cols < 16 || buf_cols % 16) return 6;
     if (d_L && ((uintptr_t)d_L & 15)) return 12;     // rows are read as float4
     if (k <= 0 || n <= 0 || k % 16 || n % 16 || col != n ||
         (long long)(k / 16) * (n / 16) > INT32_MAX || k > (1 << 22))
@@ -1018,8 +1019,8 @@ int xtq_ldlq_chain_multi_dev(const float* d_W, const float* d_L, int k, int n, i
     if (current_device(&dev)) return 1;
     rc = dev_init(dev);
     if (rc) return rc;
-    return run_ldlq_chain(g_dev[dev], d_W, d_L, k, n, grp, ngroups, c, margin, pivot, d_hatW,
-                          d_states, d_targets, (hipStream_t)stream);
+    return run_ldlq_chain(g_dev[dev], d_W, d_L, k, n, grp, ngroups, c, margin, pivot, buf_cols,
+                          d_hatW, d_states, d_targets, (hipStream_t)stream);
 }
 
 int xtq_vit_viterbi_dev(const float* dX, int nseq, int T, int K, const char* code,

@@ -103,13 +103,15 @@ hipError_t launch_lfac_quads(const float* L, int k, float* Lq, hipStream_t strea
 // values != epoch on entry; counter is one device word per launch.  Launches
 // over disjoint column ranges may run concurrently (they share Lq, Eq,
 // hatW, states and flags).  err |= 1 on a NaN target, |= 2 when a wait
-// expires after spin_limit polls, |= 4 on a runaway task loop.
+// expires after spin_limit polls, |= 4 on a runaway task loop.  buf_cols
+// (a multiple of 16) is the reference sweep's lazy-feedback buffer width,
+// which fixes the order the feedback is summed in.
 hipError_t launch_ldlq_chain(int K, const float* W, const float* Lq, int k, int n, int jc0,
                              int tnl, const uint16_t* lut16, int pivot, int n1, void* bp,
                              int nwg, float* xbuf, int xdump, float* hatW, float* Eq,
                              int32_t* states, int16_t* trellis, uint32_t* flags,
                              int32_t* counter, uint32_t epoch, int spin_limit, uint32_t* err,
-                             hipStream_t stream);
+                             int buf_cols, hipStream_t stream);
 
 // Traceback of one run from send (the state at step nsteps-1) down to step
 // `stop`.  Writes sout[q] = s_stop >> shift (nullable), the nsteps states

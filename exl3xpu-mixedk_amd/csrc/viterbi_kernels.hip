@@ -1244,15 +1244,30 @@ __global__ __launch_bounds__(64) void pack_kernel(const int32_t* __restrict__ st
 // only waits for a task taken before it, whose workgroup is running, so the
 // waits always end; columns advance independently, so the GPU is not left
 // half idle at the end of every block the way block-synchronous launches of
-// tn tiles are.  The feedback is a 16x16 product over m on the matrix
-// cores (v_mfma_f32_16x16x4_f32): wave w accumulates the 16-value groups of
-// m congruent to w mod 16, in ascending order, and the 16 wave partials are
-// added in a fixed tree -- a fixed order of this kernel, not the
-// reference's lazily buffered GEMMs; the encode of each tile is bit-exact
-// for the targets it was given (xdump exposes them).
-constexpr int kChainDepth = 4;     // feedback m-groups in flight per wave
+// tn tiles are.
+//
+// The feedback is summed in the reference's own order, so that a tile's
+// targets are bit-identical to the reference's for the same W and L
+// (quantize.py:662-686,743-744).  The reference sweeps the blocks in
+// buffers of pb = buf_cols/16 blocks aligned to the bottom block row
+// (buffer q holds blocks tk-pb(q+1) .. tk-pb*q-1) and computes block i of
+// buffer q(i) as
+//     X = (W + L[rows of buffer q(i) below i]^T E) + prod,
+//     prod = (..((0 + P_0) + P_1) + ..) + P_{q(i)-1},  P_q = L[rows of q]^T E,
+// dropping the first term for the buffer's first block; torch's CPU GEMM
+// (MKL sgemm) accumulates every such product of inner dimension <= 128 as
+// one fp32 fused multiply-add chain over the rows in ascending order, from
+// zero.  Here each buffer's 16x16 chain runs on the matrix cores:
+// v_mfma_f32_16x16x1f32 multiplies four independent 16x1 by 1x16 blocks
+// and adds each product to its accumulator with one rounding -- a fused
+// multiply-add per output per step -- so block b of a wave accumulates
+// buffer b's chain in m order exactly.  A round covers 64 buffers (4 per
+// wave); the 256 partials of each buffer go to LDS and 256 threads fold
+// them into prod in buffer order.
+constexpr int kFbPrefetch = 2;     // feedback m-quads in flight per lane
 
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 
 // Operand layout of the feedback ("quad layout"): a [k][n] matrix M is
 // stored per 16-column block b as a [k/4][16][4] array,
@@ -1290,11 +1305,11 @@ __global__ __launch_bounds__(kFwdThreads) void ldlq_chain_kernel(
     float* __restrict__ xbuf, float* __restrict__ hatW, float* __restrict__ Eq,
     int32_t* __restrict__ states, int16_t* __restrict__ trellis, uint32_t* __restrict__ flags,
     int32_t* __restrict__ counter, uint32_t epoch, int spin_limit, uint32_t* __restrict__ err,
-    int xdump) {
+    int xdump, int pbuf) {
     using G = Geom<K>;
     __shared__ FwdSmem<K, 1> sm;
-    __shared__ float part[kFwdThreads / 64][256];     // per-wave feedback partials
-    // traceback staging: the forward's b buffers where they hold 64 KiB
+    // traceback staging: the forward's b buffers where they hold 64 KiB; the
+    // feedback's per-buffer partials use the same 64 KiB before the passes
     constexpr bool kOwnStage = 2 * sizeof(float) * G::SPL < (size_t)kTbStage;
     __shared__ __attribute__((aligned(16))) uint4 tbstage[kOwnStage ? kTbStage / 16 : 1];
     uint4* const stage = kOwnStage ? tbstage : (uint4*)&sm.bbuf[0][0][0];
@@ -1358,80 +1373,92 @@ __global__ __launch_bounds__(kFwdThreads) void ldlq_chain_kernel(
         }
         __syncthreads();
         if (!__builtin_amdgcn_readfirstlane(ok)) break;
-        // targets: the feedback X_fb[r][c] = sum_m L[m][16i+r] E[m][16j+c]
-        // over m >= 16(i+1) on the matrix cores.  One MFMA 16x16x4 step
-        // takes A[r][q] from lane 16q + r and B[q][c] from lane 16q + c;
-        // lane (q, r) loads the float4 of L[m0+4q .. +3][16i+r] and of
-        // E[m0+4q .. +3][16j+r] (quad layout: one 1 KiB block per operand
-        // per wave) for a 16-value group m0 and feeds its components to 4
-        // steps (step t sums m = m0 + 4q + t over q): one 16-byte load per
-        // operand per lane and 4 MFMAs per group.  The accumulator lane
-        // (q, c) holds rows 4q..4q+3 of column c.
+        // targets in the reference's order (see above): rounds of 64 buffers,
+        // buffer b = b0 + 4 wv + (lane >> 4) in block (lane >> 4) of the
+        // wave's accumulator; lane (blk, rc) feeds row rc of L and column rc
+        // of E of that buffer, 4 consecutive m per 16-byte load (quad
+        // layout), kFbPrefetch m-quads ahead; b == qi is the part of block
+        // i's own buffer below it.
         {
-            const int wv = tid >> 6, ln = tid & 63, rr = ln & 15, qq = ln >> 4;
-            v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (Lq != nullptr && i + 1 < tk) {
-                const int mstart = 16 * (i + 1), ngr = (k - mstart) >> 4;
-                // wave-uniform operand bases (SGPRs) and 32-bit lane byte
-                // offsets; every load is issued (clamped to the last group,
-                // whose operands are then zeroed), so the waits count down
-                // through the kChainDepth groups in flight instead of
-                // draining them
-                const size_t qbase = (size_t)(mstart >> 2) * 64;
-                gbyte_t* const la = uniform_gptr((uint8_t*)(Lq + (size_t)i * 16 * k + qbase));
-                gbyte_t* const eb = uniform_gptr((uint8_t*)(Eq + (size_t)j * 16 * k + qbase));
-                const uint32_t lane = (uint32_t)(64 * qq + 4 * rr) * 4u;
-                auto goff = [&](int g) {
-                    return lane + (uint32_t)(g < ngr ? g : ngr - 1) * 1024u;
-                };
-                typedef __attribute__((address_space(1))) const v4f gv4_t;
-                v4f pa[kChainDepth], pb[kChainDepth];
-#pragma unroll
-                for (int d = 0; d < kChainDepth; ++d) {
-                    const uint32_t o = goff(wv + 16 * d);
-                    pa[d] = *(gv4_t*)(la + o);
-                    pb[d] = *(gv4_t*)(eb + o);
+            float* const P = (float*)stage;               // [64][256] partials
+            const int wv = tid >> 6, ln = tid & 63, blk = ln >> 4, rc = ln & 15;
+            const int qi = (tk - 1 - i) / pbuf, cur = tk - pbuf * qi, nbuf = qi + 1;
+            const bool has_gin = (i + 1 < cur);
+            const bool fb = (Lq != nullptr);
+            float prod = 0.0f, gin = 0.0f;
+            for (int b0 = 0; fb && b0 < nbuf; b0 += 64) {
+                const int bw = b0 + 4 * wv, b = bw + blk;
+                int mlo = 0, nq = 0;
+                if (b < qi) {
+                    mlo = 16 * (tk - pbuf * (b + 1));
+                    nq = 4 * pbuf;
+                } else if (b == qi) {
+                    mlo = 16 * (i + 1);
+                    nq = 4 * (cur - i - 1);
                 }
-                // (the compiler barriers keep the prefetches where they are:
-                // otherwise the loads feeding the loop's phis are merged into
-                // one load at the top of the loop, right before their use)
-                asm volatile("" ::: "memory");
-                for (int g0 = wv; g0 < ngr; g0 += 16 * kChainDepth) {
+                // wave-uniform step count: full buffers if the wave holds
+                // one, else block i's own buffer; shorter lanes feed zeros,
+                // whose products leave the accumulator unchanged
+                const int nqw = bw < qi ? 4 * pbuf : (bw == qi ? 4 * (cur - i - 1) : 0);
+                v16f acc;
 #pragma unroll
-                    for (int d = 0; d < kChainDepth; ++d) {
-                        const int g = g0 + 16 * d;
-                        const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
-                        const v4f a = (g < ngr) ? pa[d] : z, b = pb[d];
-                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, acc, 0, 0, 0);
-                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, acc, 0, 0, 0);
-                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, acc, 0, 0, 0);
-                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, acc, 0, 0, 0);
-                        const uint32_t o = goff(g + 16 * kChainDepth);
-                        pa[d] = *(gv4_t*)(la + o);
-                        pb[d] = *(gv4_t*)(eb + o);
-                        __builtin_amdgcn_sched_barrier(0);   // issued right after their use
+                for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+                if (nqw > 0) {
+                    typedef __attribute__((address_space(1))) const v4f gv4_t;
+                    const float* la = Lq + (size_t)i * 16 * k + (size_t)(mlo >> 2) * 64 + 4 * rc;
+                    const float* eb = Eq + (size_t)j * 16 * k + (size_t)(mlo >> 2) * 64 + 4 * rc;
+                    const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
+                    v4f pa[kFbPrefetch], pe[kFbPrefetch];
+                    // every load is issued at a valid address (clamped), its
+                    // value zeroed past the lane's buffer
+                    auto ld = [&](int sl, int mq) {
+                        const int mc = mq < nq ? mq : (nq > 0 ? nq - 1 : 0);
+                        const v4f a = *(gv4_t*)(la + mc * 64), e = *(gv4_t*)(eb + mc * 64);
+                        pa[sl] = mq < nq ? a : z;
+                        pe[sl] = mq < nq ? e : z;
+                    };
+#pragma unroll
+                    for (int p = 0; p < kFbPrefetch; ++p) ld(p, p);
+                    for (int mq0 = 0; mq0 < nqw; mq0 += kFbPrefetch) {
+#pragma unroll
+                        for (int u = 0; u < kFbPrefetch; ++u) {
+                            const v4f a = pa[u], e = pe[u];
+                            ld(u, mq0 + u + kFbPrefetch);
+                            if (mq0 + u < nqw) {
+                                acc = __builtin_amdgcn_mfma_f32_16x16x1f32(a.x, e.x, acc, 0, 0, 0);
+                                acc = __builtin_amdgcn_mfma_f32_16x16x1f32(a.y, e.y, acc, 0, 0, 0);
+                                acc = __builtin_amdgcn_mfma_f32_16x16x1f32(a.z, e.z, acc, 0, 0, 0);
+                                acc = __builtin_amdgcn_mfma_f32_16x16x1f32(a.w, e.w, acc, 0, 0, 0);
+                            }
+                        }
                     }
-                    asm volatile("" ::: "memory");
                 }
-            }
+                // accumulator register v = 4 blk' + t of lane (q, c): block
+                // blk', row 4q + t, column c
 #pragma unroll
-            for (int v = 0; v < 4; ++v) part[wv][(4 * qq + v) * 16 + rr] = acc[v];
-            __syncthreads();
+                for (int v = 0; v < 16; ++v)
+                    P[(4 * wv + (v >> 2)) * 256 + (4 * blk + (v & 3)) * 16 + rc] = acc[v];
+                __syncthreads();
+                if (tid < 256) {
+                    const int nr = (nbuf - b0) < 64 ? (nbuf - b0) : 64;
+                    for (int sl = 0; sl < nr; ++sl) {
+                        const float v = P[sl * 256 + tid];
+                        if (b0 + sl < qi) prod = prod + v;
+                        else gin = v;
+                    }
+                }
+                __syncthreads();
+            }
             if (tid < 256) {
-                float p8[8];
-#pragma unroll
-                for (int w = 0; w < 8; ++w) p8[w] = part[w][tid] + part[w + 8][tid];
-#pragma unroll
-                for (int w = 0; w < 4; ++w) p8[w] += p8[w + 4];
-                const float fb = (p8[0] + p8[2]) + (p8[1] + p8[3]);
-                // sequence order: x_t = tile[perm[t]] (quantize.py:684-686)
-                const int pe = tid;                      // tile element handled here
-                const float x = W[(size_t)(16 * i + (pe >> 4)) * n + 16 * j + (pe & 15)] + fb;
-                part[0][pe] = x;
+                const int pe = tid;                       // tile element handled here
+                const float w = W[(size_t)(16 * i + (pe >> 4)) * n + 16 * j + (pe & 15)];
+                // no factor: the targets are W itself (quantize.py:680)
+                P[pe] = !fb ? w : (has_gin ? (w + gin) + prod : w + prod);
             }
             __syncthreads();
-            // thread q writes target q; fwd_run reads it back in thread q
-            if (tid < 256) xs[tid] = part[0][tc_perm(tid)];
+            // sequence order x_t = tile[perm[t]] (quantize.py:684-686); thread
+            // q writes target q, fwd_run reads it back in thread q
+            if (tid < 256) xs[tid] = P[tc_perm(tid)];
         }
         __syncthreads();
         // pass 1: free run of the sequence rolled by pivot, traced back to
@@ -1649,11 +1676,11 @@ struct ChainL {
                           const uint16_t* lut16, int pivot, int n1, void* bp, int nwg,
                           float* xbuf, int xdump, float* hatW, float* Eq, int32_t* states,
                           int16_t* trellis, uint32_t* flags, int32_t* counter, uint32_t epoch,
-                          int spin_limit, uint32_t* err, hipStream_t s) {
+                          int spin_limit, uint32_t* err, int pbuf, hipStream_t s) {
         hipLaunchKernelGGL(reset_counter_kernel, dim3(1), dim3(1), 0, s, counter);
         hipLaunchKernelGGL(ldlq_chain_kernel<K>, dim3(nwg), dim3(kFwdThreads), 0, s, W, Lq, k,
                            n, jc0, tnl, lut16, pivot, n1, (uint8_t*)bp, xbuf, hatW, Eq, states,
-                           trellis, flags, counter, epoch, spin_limit, err, xdump);
+                           trellis, flags, counter, epoch, spin_limit, err, xdump, pbuf);
         return hipGetLastError();
     }
 };
@@ -1769,14 +1796,15 @@ hipError_t launch_ldlq_chain(int K, const float* W, const float* Lq, int k, int 
                             int nwg, float* xbuf, int xdump, float* hatW, float* Eq,
                             int32_t* states, int16_t* trellis, uint32_t* flags,
                             int32_t* counter, uint32_t epoch, int spin_limit, uint32_t* err,
-                            hipStream_t stream) {
+                            int buf_cols, hipStream_t stream) {
     if (k <= 0 || n <= 0 || tnl <= 0) return hipSuccess;
     if (k % 16 || n % 16 || jc0 < 0 || jc0 + tnl > n / 16 || pivot < 0 || pivot >= kSteps ||
-        n1 <= pivot || n1 > kSteps || nwg < 1 || spin_limit < 1)
+        n1 <= pivot || n1 > kSteps || nwg < 1 || spin_limit < 1 || buf_cols < 16 ||
+        buf_cols % 16)
         return hipErrorInvalidValue;
     return dispatch_k<ChainL>(K, W, Lq, k, n, jc0, tnl, lut16, pivot, n1, bp, nwg, xbuf, xdump,
                               hatW, Eq, states, trellis, flags, counter, epoch, spin_limit, err,
-                              stream);
+                              buf_cols / 16, stream);
 }
 
 hipError_t launch_traceback(int K, const void* bp, int nseq, const int32_t* send,

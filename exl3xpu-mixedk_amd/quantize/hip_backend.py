@@ -53,9 +53,10 @@ def lib():
         L.xtq_vit_tailbite_dev_async.argtypes = [vp, i32, i32, cp, i32, i32, vp, vp, vp]
         L.xtq_vit_tailbite_dev_noalloc.argtypes = [vp, i32, i32, cp, i32, i32, vp, vp, vp]
         L.xtq_vit_status_dev.argtypes = [vp]
-        L.xtq_ldlq_chain_dev.argtypes = [vp, vp, i32, i32, i32, cp, i32, i32, vp, vp, vp, vp, vp]
+        L.xtq_ldlq_chain_dev.argtypes = [vp, vp, i32, i32, i32, cp, i32, i32, i32, vp, vp, vp,
+                                         vp, vp]
         L.xtq_ldlq_chain_multi_dev.argtypes = [vp, vp, i32, i32, i32, vp, vp, cp, i32, i32,
-                                               vp, vp, vp, vp, vp]
+                                               i32, vp, vp, vp, vp, vp]
         L.xtq_vit_viterbi_dev.argtypes = [vp, i32, i32, i32, cp, vp, i32, vp, vp]
         L.xtq_trellis_decode_dev.argtypes = [vp, i32, i32, i32, cp, vp, vp, vp]
         L.xtq_trellis_pack_dev.argtypes = [vp, i32, i32, vp, vp]
@@ -147,12 +148,14 @@ def status(device=None):
 
 def ldlq_chain(W: torch.Tensor, L: torch.Tensor | None, K, pivot: int, margin: int,
                code: str = "mul1", states: bool = True, targets: bool = False,
-               groups=None):
+               groups=None, buf_cols: int = 128):
     """BlockLDLQ sweep of W [k, n] fp32 (inner domain, device) with the
     block-LDL factor L [k, k] (or None: no feedback) as column chains on the
-    GPU (xtq_ldlq_chain_dev).  Returns (What [k, n] fp32, states int32
-    [k/16, n/16, 256] or None, trellis int16 [k/16, n/16, 16K], targets fp32
-    [k/16, n/16, 256] or None), all on W's device.
+    GPU (xtq_ldlq_chain_dev), the feedback summed in the order of the
+    reference's ldlq_viterbi with lazy buffers of buf_cols columns.  Returns
+    (What [k, n] fp32, states int32 [k/16, n/16, 256] or None, trellis int16
+    [k/16, n/16, 16K], targets fp32 [k/16, n/16, 256] or None), all on W's
+    device.
 
     groups: None (all columns at K), or a list of (ncols, K) that splits W's
     columns into consecutive groups encoded at their own K
@@ -186,7 +189,7 @@ def ldlq_chain(W: torch.Tensor, L: torch.Tensor | None, K, pivot: int, margin: i
     with torch.cuda.device(dev):
         rc = lib().xtq_ldlq_chain_multi_dev(
             W.data_ptr(), L.data_ptr() if L is not None else None, k, n, ng, ncols, ks,
-            code_name(code).encode(), int(margin), int(pivot), hatW.data_ptr(),
+            code_name(code).encode(), int(margin), int(pivot), int(buf_cols), hatW.data_ptr(),
             st.data_ptr() if st is not None else None, ptrs,
             xt.data_ptr() if xt is not None else None, _stream(dev))
     _check("xtq_ldlq_chain_multi_dev", rc)

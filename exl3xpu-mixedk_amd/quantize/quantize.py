@@ -420,7 +420,7 @@ def ldlq_viterbi(Wq: torch.Tensor, Lfac: torch.Tensor | None, lut: torch.Tensor,
         Lg = Lfac.to(gdev, torch.float32).contiguous() if feedback else None
         hatW, states, trellis, xt = _hb.ldlq_chain(
             Wg, Lg, K, piv, int(margin), code=kcode, states=True,
-            targets=bool(ldlq_viterbi.keep_targets))
+            targets=bool(ldlq_viterbi.keep_targets), buf_cols=int(buf_cols))
         _chain_progress(progress, tk)
         ldlq_viterbi.last_trellis = trellis
         ldlq_viterbi.last_targets = xt
@@ -636,7 +636,8 @@ def quantize_linear_group(Ws, H_x: torch.Tensor | None, code: str = "exl3_mul1",
             Wq.to(gdev, torch.float32).contiguous(),
             Lfac.to(gdev, torch.float32).contiguous() if feedback else None, None, 128,
             int(margin), code=_hb.code_name(_kernel_code(lut, L)), states=True,
-            targets=bool(ldlq_viterbi.keep_targets), groups=[(r[1], r[2]) for r in runs])
+            targets=bool(ldlq_viterbi.keep_targets), groups=[(r[1], r[2]) for r in runs],
+            buf_cols=int(buf_cols))
         states = st.long().to(dev)
         hatWq = hatWq.to(dev)
         ldlq_viterbi.last_targets = xt

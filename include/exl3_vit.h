@@ -169,11 +169,17 @@ XTQ_API int xtq_vit_status_dev(void* stream);
  * never idle at the end of a 16-row block.  No reference counterpart for
  * the launch itself (the reference issues one tail-bite per 16-row block
  * with torch GEMMs for the feedback); each tile's encode is bit-exact for
- * its targets, which d_targets exposes.  The feedback sums are this
- * kernel's own fixed-order fp32 dot products.  Synchronous on return.
+ * its targets, which d_targets exposes.  The feedback is summed in the
+ * reference's own order (quantize.py:662-686,743-744 with buf_cols, its
+ * GEMMs evaluated as torch's CPU sgemm does: one fp32 fused multiply-add
+ * chain per output over the rows of each buffer, buffers added in sweep
+ * order), so the targets, and hence W_hat and the trellis, equal the
+ * reference's ldlq_viterbi on the same W and L.  Synchronous on return.
  *   d_W       [k][n] fp32 device, inner domain (k, n multiples of 16)
  *   d_L       [k][k] fp32 device block-LDL factor (row-major, 16-byte
  *             aligned), or NULL for no feedback
+ *   buf_cols  ldlq_viterbi's lazy-feedback buffer width (a multiple of 16;
+ *             the reference's default is 128), else status 6
  *   d_hatW    [k][n] fp32 device (out): the decoded tiles
  *   d_states  [k/16 * n/16][256] int32 device (out), or NULL
  *   d_trellis [k/16][n/16][16K] int16 device (out)
@@ -181,9 +187,9 @@ XTQ_API int xtq_vit_status_dev(void* stream);
  *             sequence order), or NULL
  */
 XTQ_API int xtq_ldlq_chain_dev(const float* d_W, const float* d_L, int k, int n, int K,
-                               const char* code, int margin, int pivot, float* d_hatW,
-                               int32_t* d_states, int16_t* d_trellis, float* d_targets,
-                               void* stream);
+                               const char* code, int margin, int pivot, int buf_cols,
+                               float* d_hatW, int32_t* d_states, int16_t* d_trellis,
+                               float* d_targets, void* stream);
 
 /*
  * xtq_ldlq_chain_dev for weights quantized side by side at different K
@@ -197,9 +203,10 @@ XTQ_API int xtq_ldlq_chain_dev(const float* d_W, const float* d_L, int k, int n,
  */
 XTQ_API int xtq_ldlq_chain_multi_dev(const float* d_W, const float* d_L, int k, int n,
                                      int ngroups, const int* h_ncols, const int* h_K,
-                                     const char* code, int margin, int pivot, float* d_hatW,
-                                     int32_t* d_states, int16_t* const* h_trellis,
-                                     float* d_targets, void* stream);
+                                     const char* code, int margin, int pivot, int buf_cols,
+                                     float* d_hatW, int32_t* d_states,
+                                     int16_t* const* h_trellis, float* d_targets,
+                                     void* stream);
 
 /*
  * Device-pointer single Viterbi run: the HIP counterpart of viterbi()

@@ -6,6 +6,7 @@ the GPU host):
 
     python tests/golden/make_golden.py /root/reference/quantize
     python tests/golden/make_golden.py /root/reference/quantize --ties
+    python tests/golden/make_golden.py /root/reference/quantize --mid
 
 It imports the reference quantizer module (quantize/quantize.py) on CPU and
 records input/output vectors for the functions that closed forms, invariants
@@ -22,11 +23,18 @@ and brute force cannot pin:
 --ties writes ties.npz alone: quantize_seq_tailbite on 24 sequences per K
 whose results hinge on exact cost ties (six kinds, tie_forcing_inputs) at four
 pivot/margin pairs, and viterbi() pinned and back_from runs on them.
+--mid writes e2e_mid.npz alone: quantize_linear with BlockLDLQ on a
+1024x1024 weight (4,096 tiles, 64 blocks of feedback) against the Hessian
+H[i][j] = 2^-|i-j| (exact in fp32), at K=4 and at K=5 with channel scales:
+trellis, suh, svh, Wscale, the proxy loss (fp32 as the reference computes it,
+and in fp64), a SHA-256 digest of W_hat, and a digest of the generating host's
+per-output-channel RMS reduction (channel scales depend on it).
 Only data (inputs and expected outputs) is written, as compressed .npz files
 loadable with numpy.load(allow_pickle=False).
 """
 from __future__ import annotations
 
+import hashlib
 import os
 import sys
 import time
@@ -115,6 +123,50 @@ def main_ties(refdir: str):
         data[f"VB_K{K}"] = xq.viterbi(Xt[:200], lut, K, 16, back_from=60).numpy().astype(np.int32)
         print(f"  ties K={K} done {time.time() - t0:.1f}s", flush=True)
     np.savez_compressed(os.path.join(OUT, "ties.npz"), **data)
+
+
+def kms_hessian(d: int) -> np.ndarray:
+    """H[i][j] = 2^-|i-j| (the AR(1) correlation at rho = 1/2): every entry a
+    power of two, so the fp32 matrix is exact and the same on every host."""
+    i = np.arange(d)
+    return np.ldexp(1.0, -np.abs(i[:, None] - i[None, :])).astype(np.float32)
+
+
+def main_mid(refdir: str):
+    sys.path.insert(0, refdir)
+    import quantize as xq  # the reference module, CPU only
+    torch.set_num_threads(8)
+    t0 = time.time()
+    rng = np.random.default_rng(20261202)
+    W16 = (0.02 * rng.standard_normal((1024, 1024))).astype(np.float16)
+    H = kms_hessian(1024)
+    data = {"W16": W16}
+    W = torch.from_numpy(W16.astype(np.float32))
+    Ht = torch.from_numpy(H)
+    # the channel-scale path reduces W with torch CPU means, whose rounding
+    # depends on the host CPU: a digest of this host's per-output-channel RMS
+    # lets a test tell whether its own host reduces identically
+    W32 = W.t().contiguous()
+    data["rout_sha256"] = np.frombuffer(hashlib.sha256(
+        W32.square().mean(dim=0).sqrt().numpy().tobytes()).digest(), dtype=np.uint8)
+    for tag, K, cs in (("k4", 4, False), ("k5cs", 5, True)):
+        r = xq.quantize_linear(W, Ht, code="exl3_mul1", K=K, use_ldlq=True, margin=0,
+                               channel_scales=cs, device="cpu")
+        data[f"{tag}_trellis"] = r["trellis"].numpy()
+        data[f"{tag}_suh"] = r["suh"].float().numpy()
+        data[f"{tag}_svh"] = r["svh"].float().numpy()
+        data[f"{tag}_Wscale"] = np.float32(r["Wscale"])
+        data[f"{tag}_herr"] = np.float64(xq.hessian_weighted_err(W, r["W_hat"], Ht))
+        # the same proxy loss in fp64 (its fp32 einsum rounds by the host's
+        # reduction order) and a digest of W_hat's bytes
+        dW = (r["W_hat"] - W).double()
+        H64 = Ht.double()
+        data[f"{tag}_herr64"] = np.float64(((dW @ H64) * dW).sum() /
+                                           ((W.double() @ H64) * W.double()).sum())
+        data[f"{tag}_What_sha256"] = np.frombuffer(
+            hashlib.sha256(r["W_hat"].contiguous().numpy().tobytes()).digest(), dtype=np.uint8)
+        print(f"  mid {tag} done {time.time() - t0:.1f}s", flush=True)
+    np.savez_compressed(os.path.join(OUT, "e2e_mid.npz"), **data)
 
 
 def main(refdir: str):
@@ -219,5 +271,7 @@ if __name__ == "__main__":
     ref = args[0] if args else "/root/reference/quantize"
     if "--ties" in sys.argv[1:]:
         main_ties(ref)
+    elif "--mid" in sys.argv[1:]:
+        main_mid(ref)
     else:
         main(ref)

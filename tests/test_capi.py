@@ -75,19 +75,21 @@ def test_status_codes_without_device(lib):
     assert lib.xtq_trellis_pack_dev(fake, 1, 3, None, None) == 12
     ch = lib.xtq_ldlq_chain_dev
     mis = ctypes.c_void_p(20)           # not 16-byte aligned
-    assert ch(fake, fake, 64, 64, 8, b"mul1", 0, 128, fake, None, fake, None, None) == 9
-    assert ch(fake, fake, 64, 64, 4, b"mul1", 0, 256, fake, None, fake, None, None) == 10
-    assert ch(fake, fake, 64, 64, 4, b"qtip", 0, 128, fake, None, fake, None, None) == 8
-    assert ch(None, fake, 64, 64, 4, b"mul1", 0, 128, fake, None, fake, None, None) == 12
-    assert ch(fake, fake, 64, 64, 4, b"mul1", 0, 128, fake, None, None, None, None) == 12
-    assert ch(fake, mis, 64, 64, 4, b"mul1", 0, 128, fake, None, fake, None, None) == 12
-    assert ch(fake, fake, 72, 64, 4, b"mul1", 0, 128, fake, None, fake, None, None) == 6
-    assert ch(fake, None, 64, 0, 4, b"mul1", 0, 128, fake, None, fake, None, None) == 6
+    assert ch(fake, fake, 64, 64, 8, b"mul1", 0, 128, 128, fake, None, fake, None, None) == 9
+    assert ch(fake, fake, 64, 64, 4, b"mul1", 0, 256, 128, fake, None, fake, None, None) == 10
+    assert ch(fake, fake, 64, 64, 4, b"qtip", 0, 128, 128, fake, None, fake, None, None) == 8
+    assert ch(None, fake, 64, 64, 4, b"mul1", 0, 128, 128, fake, None, fake, None, None) == 12
+    assert ch(fake, fake, 64, 64, 4, b"mul1", 0, 128, 128, fake, None, None, None, None) == 12
+    assert ch(fake, mis, 64, 64, 4, b"mul1", 0, 128, 128, fake, None, fake, None, None) == 12
+    assert ch(fake, fake, 72, 64, 4, b"mul1", 0, 128, 128, fake, None, fake, None, None) == 6
+    assert ch(fake, None, 64, 0, 4, b"mul1", 0, 128, 128, fake, None, fake, None, None) == 6
+    assert ch(fake, None, 64, 64, 4, b"mul1", 0, 128, 24, fake, None, fake, None, None) == 6
+    assert ch(fake, None, 64, 64, 4, b"mul1", 0, 128, 0, fake, None, fake, None, None) == 6
     chm = lib.xtq_ldlq_chain_multi_dev
     i2 = (ctypes.c_int * 2)
     tp2 = (ctypes.c_void_p * 2)(16, 16)
     tp1 = (ctypes.c_void_p * 2)(16, None)
-    args = (b"mul1", 0, 128, fake, None)
+    args = (b"mul1", 0, 128, 128, fake, None)
     assert chm(fake, None, 64, 64, 2, i2(32, 32), i2(4, 9), *args, tp2, None, None) == 9
     assert chm(fake, None, 64, 64, 2, i2(32, 24), i2(4, 7), *args, tp2, None, None) == 6
     assert chm(fake, None, 64, 64, 2, i2(32, 16), i2(4, 7), *args, tp2, None, None) == 6

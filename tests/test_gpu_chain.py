@@ -2,11 +2,14 @@
 
 The chain kernel computes every tile's targets itself, from the decoded
 tiles below it in its column, and encodes them.  The tests check
-  * every tile's targets against the BlockLDLQ target formula of
-    quantize.py:662-686 (X = W[block] + L[later, block]^T (W - What)[later])
-    evaluated in fp64 from the kernel's own What, within the rounding bound
-    of the kernel's fp32 sums -- a wrong index, sign or row range of the
-    feedback misses it by orders of magnitude;
+  * every tile's targets bit for bit against the reference's own fp32
+    sweep (quantize.py:662-686,743-744, torch CPU GEMMs) on the kernel's
+    What, and against the target formula X = W[block] + L[later, block]^T
+    (W - What)[later] evaluated in fp64, within the rounding bound of the
+    fp32 sums -- a wrong index, sign or row range of the feedback misses it
+    by orders of magnitude;
+  * the whole sweep against the reference's block schedule on the CPU on
+    the same inputs, What and states bit for bit;
   * every tile's states bit for bit against the oracle on those targets, and
     the packed trellis against the oracle's packing;
   * decode(trellis) == What;
@@ -50,13 +53,45 @@ def _seq_order(T: torch.Tensor, perm: torch.Tensor) -> torch.Tensor:
     return tiles[..., perm]
 
 
+def _ref_targets(Wq, Lf, hatW, perm, buf_cols=128):
+    """Every tile's targets [k/16, n/16, 256] as the reference's ldlq_viterbi
+    computes them (quantize.py:662-686,743-744: lazily buffered feedback,
+    torch CPU GEMMs), given the final What (the error of the rows below a
+    block is final when the block is swept)."""
+    k, n = Wq.shape
+    tk, per = k // 16, max(1, buf_cols // 16)
+    W_t, hatW_t = Wq.t().contiguous(), hatW.t().contiguous()
+    prod = torch.zeros(k, n)
+    X = torch.empty(tk, n // 16, 256)
+    for cur in range(tk, 0, -per):
+        lo = max(0, cur - per)
+        for i in range(cur - 1, lo - 1, -1):
+            c0, c1 = 16 * i, 16 * (i + 1)
+            rows = W_t[:, c0:c1].t().contiguous()
+            if c1 < 16 * cur:
+                err = (W_t[:, c1:16 * cur] - hatW_t[:, c1:16 * cur]).t()
+                rows = rows + Lf[c1:16 * cur, c0:c1].t() @ err
+            rows = rows + prod[c0:c1, :]
+            X[i] = rows.view(16, n // 16, 16).permute(1, 0, 2).reshape(n // 16, 256)[:, perm]
+        if lo > 0:
+            err = (W_t[:, 16 * lo:16 * cur] - hatW_t[:, 16 * lo:16 * cur]).t()
+            prod += Lf[16 * lo:16 * cur, :].t() @ err
+    return X
+
+
 def _check_targets(W, L, hatW, xt, perm):
-    """xt against the fp64 formula on the kernel's What.  The kernel sums each
-    target as 16 fp32 wave partials of at most k/16 products each (matrix-core
-    steps of 4 products), adds them in a 4-level tree and then W: even with a
-    rounding after every product its error is below (k/16 + 5) u times
-    |W| + sum |L| |E| (u = 2^-24); the check allows (k/4 + 36) u."""
+    """xt against the fp64 formula on the kernel's What, within a rounding
+    bound, and bit for bit against the reference's own fp32 sweep on the
+    kernel's What (the kernel sums in that order).  Each feedback term is
+    one fused multiply-add chain of at most 128 products, the chains are
+    added one after another (k/128 of them) and then W: the error is below
+    (128 + k/128 + 3) u times |W| + sum |L| |E| (u = 2^-24)."""
     k, n = W.shape
+    if L is not None:
+        assert torch.equal(xt, _ref_targets(W, L, hatW, perm)), \
+            "targets differ from the reference's sweep on the same What"
+    else:
+        assert torch.equal(xt, _seq_order(W, perm)), "targets without feedback != W"
     W64 = W.double()
     E = (W - hatW).double()              # the kernel's fp32 E, exactly
     X64, B = W64.clone(), W64.abs()
@@ -67,7 +102,7 @@ def _check_targets(W, L, hatW, xt, perm):
             X64[r0:r1] += L64[r1:, r0:r1].t() @ E[r1:]
             B[r0:r1] += L64[r1:, r0:r1].abs().t() @ E[r1:].abs()
     d = (xt.double() - _seq_order(X64, perm)).abs()
-    lim = (k / 4 + 36) * U32 * _seq_order(B, perm)
+    lim = (128 + k / 128 + 3) * U32 * _seq_order(B, perm)
     assert (d <= lim).all(), f"worst excess {float((d - lim).max()):.3e}"
     return float(d.max())
 
@@ -321,10 +356,8 @@ def test_chain_targets_vs_golden_pinned_block_path(xq, hb, monkeypatch, cpu8):
     """The reference's own 128x128 AR(1) case: the block schedule with the
     torch work on the CPU reproduces the reference's golden trellis bit for
     bit, so its per-launch targets are the reference's.  The chain, fed the
-    same inner weights and factor, must produce those targets within the
-    fp32 rounding of the two summation orders wherever the tiles below in the
-    column encoded identically (so E agrees), and exactly W for the first
-    block row swept."""
+    same inner weights and factor, produces those targets bit for bit, and
+    so the golden trellis and the block schedule's What."""
     from conftest import load_golden
     e = load_golden("e2e_128.npz")
     W, H = torch.from_numpy(e["W"]), torch.from_numpy(e["H_ar"])
@@ -333,7 +366,9 @@ def test_chain_targets_vs_golden_pinned_block_path(xq, hb, monkeypatch, cpu8):
 
     def rec_ldlq(Wq, Lfac, *a, **kw):
         seen["Wq"], seen["Lfac"] = Wq.clone(), Lfac.clone()
-        return real_ldlq(Wq, Lfac, *a, **kw)
+        out = real_ldlq(Wq, Lfac, *a, **kw)
+        seen["hatW"] = out[0].clone()
+        return out
 
     def rec_launch(X, K, code, pivot, margin):
         launches.append(X.detach().cpu().clone())
@@ -347,34 +382,37 @@ def test_chain_targets_vs_golden_pinned_block_path(xq, hb, monkeypatch, cpu8):
     r = xq.quantize_linear(W, H, code="exl3_mul1", K=4, use_ldlq=True, margin=0, device="cpu")
     np.testing.assert_array_equal(r["trellis"].numpy(), e["ar_trellis"])      # pinned
     Wq, Lf = seen["Wq"], seen["Lfac"]
-    k, n = Wq.shape
-    tk, tn = k // 16, n // 16
     Xb = torch.stack(launches[::-1])                       # [tk, tn, 256], block i first
     print("case golden 128x128 AR(1): chain on the GPU", flush=True)
     hatW, st, tr, xt = (t.cpu() for t in hb.ldlq_chain(Wq.cuda(), Lf.cuda(), 4, 128, 0,
                                                         targets=True))
-    perm = xq.tensor_core_perm()
-    assert torch.equal(xt[tk - 1], Xb[tk - 1])            # no feedback: exactly W
-    same = (tr == torch.from_numpy(e["ar_trellis"])).all(dim=-1)              # [tk, tn]
-    # |x_chain - x_block| <= (k/4 + 36 + k) u (|W| + sum |L| |E|)
-    E = (Wq - hatW).double()
-    B = Wq.double().abs()
-    L64 = Lf.double()
-    for i in range(tk - 1):
-        B[16 * i:16 * (i + 1)] += L64[16 * (i + 1):, 16 * i:16 * (i + 1)].abs().t() @ \
-            E[16 * (i + 1):].abs()
-    lim = (k / 4 + 36 + k) * U32 * _seq_order(B, perm)
-    checked = 0
-    for j in range(tn):
-        for i in range(tk - 2, -1, -1):
-            if not bool(same[i + 1:, j].all()):
-                break
-            d = (xt[i, j].double() - Xb[i, j].double()).abs()
-            assert bool((d <= lim[i, j]).all()), (i, j, float((d - lim[i, j]).max()))
-            checked += 1
-    print(f"tiles identical to the golden trellis: {int(same.sum())}/{tk * tn}, "
-          f"targets checked: {checked}")
-    assert checked >= (tk - 1) * tn // 2
+    assert torch.equal(xt, Xb), "chain targets != the reference's per-launch targets"
+    np.testing.assert_array_equal(tr.numpy(), e["ar_trellis"])
+    assert torch.equal(hatW, seen["hatW"])
+
+
+@pytest.mark.parametrize("K,shape", [(4, (4096, 4096)), (6, (2048, 1024)), (2, (1024, 512))])
+def test_chain_equals_cpu_block_schedule(xq, hb, cpu8, K, shape):
+    """ldlq_viterbi on the same inner weights and factor: the column chains on
+    the GPU against the reference's block schedule with its torch feedback on
+    the CPU (the reference's arithmetic; each launch's encode on the GPU is
+    pinned separately): identical What and states for every tile, up to a
+    4096x4096 weight (256 blocks of feedback, 65,536 tiles)."""
+    import workloads as wl
+    k, n = shape
+    g = torch.Generator().manual_seed(20 + K)
+    Wq = torch.randn(k, n, generator=g)
+    G = wl.ar1_gram(k, 2 * k, 0.5, 20 + K)
+    G.diagonal().add_(0.01 * G.diagonal().mean())
+    Lf, _ = xq.block_LDL(G, 16)
+    lut = xq.get_lut("exl3_mul1")
+    print(f"case chain vs CPU block schedule {k}x{n} K={K}", flush=True)
+    hb_, sb = xq.ldlq_viterbi(Wq, Lf, lut, K, 16, margin=0, schedule="block")
+    hc, sc = xq.ldlq_viterbi(Wq.cuda(), Lf.cuda(), lut.cuda(), K, 16, margin=0,
+                             schedule="chain")
+    bad = int((sc.cpu() != sb).any(dim=-1).sum())
+    assert bad == 0, f"{bad} of {sb.shape[0] * sb.shape[1]} tiles differ"
+    assert torch.equal(hc.cpu(), hb_)
 
 
 def test_chain_factor_over_2g_elements(hb, oracle_mod, mul1_lut):
