@@ -1298,6 +1298,38 @@ __global__ __launch_bounds__(256) void lfac_quads_kernel(const float* __restrict
     }
 }
 
+// ------------------------------------------------- block-128 Hadamard
+// out[128b + r][c] = sum_{t=0..127} h[r][t] * in[128b + t][c] (had_left,
+// quantize.py:134-138), evaluated as torch's CPU sgemm evaluates it: one
+// fp32 fused multiply-add chain per output over t ascending, from zero
+// (measured bit for bit against an fmaf chain).  h is the caller's
+// normalised Sylvester matrix, which is symmetric, so h[r][t] = h[t][r] and
+// the 16 multipliers a wave needs at step t are one contiguous, wave-uniform
+// row segment (scalar loads).  Wave: 16 rows x 64 columns; workgroup: 4 waves.
+__global__ __launch_bounds__(256) void had_left_kernel(const float* __restrict__ h,
+                                                       const float* __restrict__ in,
+                                                       float* __restrict__ out, int cols) {
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), ln = threadIdx.x & 63;
+    const int c = blockIdx.x * 64 + ln;
+    const int r0 = (blockIdx.z * 4 + wv) * 16;
+    const bool live = c < cols;
+    const float* src = in + (size_t)blockIdx.y * 128 * cols + (live ? c : 0);
+    float acc[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) acc[q] = 0.0f;
+    for (int t = 0; t < 128; ++t) {
+        const float w = src[(size_t)t * cols];
+        const float* hr = h + t * 128 + r0;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) acc[q] = __builtin_fmaf(hr[q], w, acc[q]);
+    }
+    if (live) {
+        float* dst = out + ((size_t)blockIdx.y * 128 + r0) * cols + c;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) dst[(size_t)q * cols] = acc[q];
+    }
+}
+
 template <int K>
 __global__ __launch_bounds__(kFwdThreads) void ldlq_chain_kernel(
     const float* __restrict__ W, const float* __restrict__ Lq, int k, int n, int jc0, int tnl,
@@ -1781,6 +1813,15 @@ hipError_t launch_tailbite_fused(int K, const float* X, int nseq, const uint16_t
         return hipErrorInvalidValue;
     return dispatch_k<FusedL>(K, X, nseq, lut16, pivot, n1, bp, send, ovbuf, flags, counter,
                               epoch, spin_limit, err, stream);
+}
+
+hipError_t launch_had_left(const float* h, const float* in, float* out, int rows, int cols,
+                           hipStream_t stream) {
+    if (rows <= 0 || cols <= 0) return hipSuccess;
+    if (rows % 128 || rows / 128 > 65535) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(had_left_kernel, dim3((cols + 63) / 64, rows / 128, 2), dim3(256), 0,
+                       stream, h, in, out, cols);
+    return hipGetLastError();
 }
 
 hipError_t launch_lfac_quads(const float* L, int k, float* Lq, hipStream_t stream) {

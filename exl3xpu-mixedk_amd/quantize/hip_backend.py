@@ -62,6 +62,7 @@ def lib():
         L.xtq_trellis_pack_dev.argtypes = [vp, i32, i32, vp, vp]
         L.xtq_trellis_unpack_dev.argtypes = [vp, i32, i32, vp, vp]
         L.xtq_vit_get_lut.argtypes = [cp, vp]
+        L.xtq_had128_left_dev.argtypes = [vp, vp, vp, i32, i32, vp]
         L.xtq_vit_scratch_per_seq.argtypes = [i32]
         L.xtq_vit_scratch_per_seq.restype = i64
         L.xtq_vit_chunk_seqs.argtypes = [i32, i32, ctypes.POINTER(ctypes.c_int)]
@@ -78,7 +79,7 @@ def lib():
                    "xtq_vit_tailbite_dev_async", "xtq_vit_tailbite_dev_noalloc", "xtq_vit_status_dev", "xtq_vit_viterbi_dev",
                    "xtq_ldlq_chain_dev", "xtq_ldlq_chain_multi_dev",
                    "xtq_trellis_decode_dev", "xtq_trellis_pack_dev",
-                   "xtq_trellis_unpack_dev", "xtq_vit_get_lut"):
+                   "xtq_trellis_unpack_dev", "xtq_vit_get_lut", "xtq_had128_left_dev"):
             getattr(L, fn).restype = i32
         _LIB = L
     return _LIB
@@ -248,6 +249,26 @@ def decode(trellis: torch.Tensor, K: int, code: str = "mul1",
             out.data_ptr() if dtype == torch.float32 else None,
             out.data_ptr() if dtype == torch.float16 else None, _stream(tr.device))
     _check("xtq_trellis_decode_dev", rc)
+    return out
+
+
+def had128_left(w: torch.Tensor, h: torch.Tensor) -> torch.Tensor:
+    """blockdiag(h) @ w for w [k, n] fp32 (device, k a multiple of 128), h
+    the normalised 128x128 Sylvester matrix on the same device: each output
+    one fused multiply-add chain in ascending order, as torch's CPU sgemm
+    evaluates the reference's matmul (xtq_had128_left_dev)."""
+    w = _dev_tensor(w, torch.float32, "w")
+    h = _dev_tensor(h, torch.float32, "h")
+    if w.dim() != 2 or w.shape[0] % 128 or h.shape != (128, 128) or h.device != w.device:
+        raise ValueError(f"had128_left needs w [128m, n] and h [128, 128] on one device, got "
+                         f"{tuple(w.shape)}, {tuple(h.shape)}")
+    out = torch.empty_like(w)
+    if w.numel() == 0:
+        return out
+    with torch.cuda.device(w.device):
+        rc = lib().xtq_had128_left_dev(h.data_ptr(), w.data_ptr(), out.data_ptr(), w.shape[0],
+                                       w.shape[1], _stream(w.device))
+    _check("xtq_had128_left_dev", rc)
     return out
 
 

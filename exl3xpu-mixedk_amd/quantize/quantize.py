@@ -132,16 +132,25 @@ def hadamard128(device=None, dtype=torch.float32) -> torch.Tensor:
 
 
 def had_left(w: torch.Tensor, h: torch.Tensor) -> torch.Tensor:
-    """Block-128 Hadamard applied on the first (k) dim of w [k, n]."""
+    """Block-128 Hadamard applied on the first (k) dim of w [k, n]
+    (quantize.py:134-138).  GPU tensors go through the library's kernel,
+    which accumulates every output in the order torch's CPU matmul does, so
+    both devices give the reference's bits."""
     k, n = w.shape
     assert k % 128 == 0
+    if w.is_cuda and w.dtype == torch.float32:
+        return _hb.had128_left(w.contiguous(), h.to(w.device, torch.float32).contiguous())
     return torch.matmul(h, w.view(k // 128, 128, n)).view(k, n)
 
 
 def had_right(w: torch.Tensor, h: torch.Tensor) -> torch.Tensor:
-    """Block-128 Hadamard applied on the last (n) dim of w [k, n]."""
+    """Block-128 Hadamard applied on the last (n) dim of w [k, n]
+    (quantize.py:141-145); on the GPU the left transform of the transpose
+    (h is symmetric: the same products in the same order)."""
     k, n = w.shape
     assert n % 128 == 0
+    if w.is_cuda and w.dtype == torch.float32:
+        return had_left(w.t().contiguous(), h).t().contiguous()
     return torch.matmul(w.view(k, n // 128, 128), h).view(k, n)
 
 
@@ -511,7 +520,8 @@ def quantize_linear(W: torch.Tensor, H_x: torch.Tensor | None, code: str = "exl3
                     use_ldlq: bool = True, device: str = "cpu",
                     batch: int = 0, dtype: torch.dtype = torch.float32,
                     margin: int = 0, compiled: bool = False, progress=None,
-                    backend: str = "hip", channel_scales: bool = False):
+                    backend: str = "hip", channel_scales: bool = False,
+                    reference_arithmetic: bool = False):
     """Quantize one nn.Linear weight (quantize.py:750-875).
 
     W [out, in]; H_x [in, in] undamped input Gram or None.  `device` is where
@@ -520,12 +530,20 @@ def quantize_linear(W: torch.Tensor, H_x: torch.Tensor | None, code: str = "exl3
     kernels always run on the GPU.  Returns a dict with W_hat [out, in] fp32,
     trellis int16 [in/16, out/16, 16K], suh/svh fp16 and diagnostics.
     channel_scales=True applies EXL3 1.4.2's per-channel scaling order.
+
+    On the GPU the Hadamard transforms and the LDLQ feedback already round as
+    the reference's CPU arithmetic does; its reductions (channel RMS, Wscale,
+    the damping mean) and the block-LDL factorisation (which the reference
+    always runs on the CPU) round differently there.  reference_arithmetic=
+    True runs those on the host CPU, as torch computes them for the
+    reference, so that with device="cuda" every result equals the reference's
+    device="cpu" result on the same host bit for bit.
     """
     return quantize_linear_group(
         [W], H_x, code=code, K=K, L=L, V=V, percdamp=percdamp, su_seed=su_seed,
         buf_cols=buf_cols, use_ldlq=use_ldlq, device=device, batch=batch, dtype=dtype,
         margin=margin, compiled=compiled, progress=progress, backend=backend,
-        channel_scales=channel_scales)[0]
+        channel_scales=channel_scales, reference_arithmetic=reference_arithmetic)[0]
 
 
 def quantize_linear_group(Ws, H_x: torch.Tensor | None, code: str = "exl3_mul1",
@@ -534,7 +552,8 @@ def quantize_linear_group(Ws, H_x: torch.Tensor | None, code: str = "exl3_mul1",
                           use_ldlq: bool = True, device: str = "cpu",
                           batch: int = 0, dtype: torch.dtype = torch.float32,
                           margin: int = 0, compiled: bool = False, progress=None,
-                          backend: str = "hip", channel_scales: bool = False):
+                          backend: str = "hip", channel_scales: bool = False,
+                          reference_arithmetic: bool = False):
     """quantize_linear for several weights that read the same input (one
     H_x, e.g. the q/k/v or gate/up projections of a layer).  K is one bit
     width for all members or one per member (mixed-K, e.g. q at 5 and k/v
@@ -548,7 +567,7 @@ def quantize_linear_group(Ws, H_x: torch.Tensor | None, code: str = "exl3_mul1",
     compute-unit count) then share the GPU instead of leaving most of it
     idle, and members of different K run as concurrent launches over a split
     of the compute units.  Returns the list of quantize_linear result dicts,
-    in order.
+    in order.  reference_arithmetic: see quantize_linear.
     """
     Ws = list(Ws)
     if not Ws:
@@ -567,6 +586,12 @@ def quantize_linear_group(Ws, H_x: torch.Tensor | None, code: str = "exl3_mul1",
     lut = get_lut(code, L).to(torch.float32)
     V = 1 if V == 0 else V
     lut_rms = lut.double().square().mean().sqrt().float()
+    # the reference's reductions and factorisation on the host CPU
+    host = bool(reference_arithmetic) and dev.type != "cpu"
+
+    def red(t: torch.Tensor) -> torch.Tensor:
+        """Where a reduction runs: the host CPU under reference_arithmetic."""
+        return _to_host(t) if host else t
 
     suh0 = sign_vec(k_in, su_seed, dev).half()
     h = hadamard128(dev, torch.float32)
@@ -579,21 +604,22 @@ def quantize_linear_group(Ws, H_x: torch.Tensor | None, code: str = "exl3_mul1",
         mb = {"n": m_out}
         if channel_scales:
             su, sv = suh.float(), svh.float()
-            r_out = W32.square().mean(dim=0).sqrt()
+            r_out = red(W32).square().mean(dim=0).sqrt()
             rm = r_out.mean()
             if rm > 1e-30:
                 r_out = r_out / rm
             zero_out = r_out.abs() < 1e-30
-            r_out = torch.where(zero_out, torch.full_like(r_out, 0.1), r_out)
+            r_out = torch.where(zero_out, torch.full_like(r_out, 0.1), r_out).to(dev)
+            zero_out = zero_out.to(dev)
             w = had_right(W32 / (sv * r_out).unsqueeze(0), h)
-            r_in = w.square().mean(dim=1).sqrt()
-            r_in = torch.where(r_in.abs() < 1e-30, torch.full_like(r_in, 0.1), r_in)
+            r_in = red(w).square().mean(dim=1).sqrt()
+            r_in = torch.where(r_in.abs() < 1e-30, torch.full_like(r_in, 0.1), r_in).to(dev)
             W_i = had_left(w / (su * r_in).unsqueeze(1), h)
             svh_store = torch.where(zero_out, torch.zeros_like(r_out), r_out)
             mb.update(su=su, sv=sv, r_in=r_in, svh_store=svh_store)
         else:
             W_i = to_inner(W32, suh, svh, h)
-        Wscale = W_i.square().mean().sqrt() / lut_rms
+        Wscale = (red(W_i).square().mean().sqrt() / lut_rms).to(dev)
         mb.update(Wq=W_i / Wscale, Wscale=Wscale, suh=suh, svh=svh)
         members.append(mb)
     Wq = members[0]["Wq"] if len(members) == 1 else \
@@ -606,8 +632,9 @@ def quantize_linear_group(Ws, H_x: torch.Tensor | None, code: str = "exl3_mul1",
         dead = G.diagonal() == 0
         if dead.any():
             G[dead, dead] = 1.0
-        G.diagonal().add_(percdamp * G.diagonal().mean())
-        Lfac = _factor_hessian(G).to(dev, Wq.dtype)
+        G.diagonal().add_((percdamp * red(G.diagonal()).mean()).to(dev))
+        # the reference factors on the CPU on every device (quantize.py:816)
+        Lfac = _factor_hessian(red(G)).to(dev, Wq.dtype)
         del G
         if progress is not None:
             progress("hinv", time.time() - t0)

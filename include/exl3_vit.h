@@ -243,6 +243,19 @@ XTQ_API int xtq_trellis_unpack_dev(const int16_t* d_trellis, int nt, int K, int3
                            void* stream);
 
 /*
+ * Device-pointer block-128 Hadamard on the first dimension: the HIP
+ * counterpart of had_left (quantize.py:134-138), d_out = blockdiag(d_h) @ d_in
+ * for [rows][cols] fp32 row-major buffers (rows a multiple of 128, d_out not
+ * d_in), d_h the [128][128] normalised Sylvester matrix of hadamard128
+ * (quantize.py:123-131).  Each output is one fp32 fused multiply-add chain
+ * over the 128 products in ascending order, as torch's CPU sgemm evaluates
+ * the reference's matmul, so results equal the reference's CPU results bit
+ * for bit.  had_right is this entry on the transpose.  Stream-ordered.
+ */
+XTQ_API int xtq_had128_left_dev(const float* d_h, const float* d_in, float* d_out, int rows,
+                                int cols, void* stream);
+
+/*
  * Copies the fp32 decode table of `code` (65536 entries) into host memory
  * (the values get_lut returns, quantize.py:90-97).
  */

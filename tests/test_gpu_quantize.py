@@ -135,6 +135,80 @@ def test_quantize_linear_mid_on_gpu_vs_reference(xq, tag, K, cs):
     assert differ <= 0.05 and rel <= 1e-3
 
 
+@pytest.mark.parametrize("tag,K,cs", [("k4", 4, False), ("k5cs", 5, True)])
+def test_reference_arithmetic_on_gpu_vs_golden(xq, cpu8, tag, K, cs):
+    """quantize_linear on the GPU with reference_arithmetic=True (the
+    reductions and the block-LDL factorisation on the host CPU, everything
+    else on the GPU) against the reference's own 1024x1024 result
+    (e2e_mid.npz): identical trellis, suh, svh, Wscale and W_hat, on hosts
+    that reduce as the generating host did (see the device="cpu" test)."""
+    e = load_golden("e2e_mid.npz")
+    W = torch.from_numpy(e["W16"].astype(np.float32))
+    H = _kms_hessian(1024)
+    same_host = hashlib.sha256(W.t().contiguous().square().mean(dim=0).sqrt().numpy()
+                               .tobytes()).digest() == e["rout_sha256"].tobytes()
+    print(f"case quantize_linear 1024x1024 {tag} device=cuda reference_arithmetic", flush=True)
+    r = xq.quantize_linear(W.cuda(), H.cuda(), code="exl3_mul1", K=K, use_ldlq=True, margin=0,
+                           channel_scales=cs, device="cuda", reference_arithmetic=True)
+    badm = (r["trellis"].numpy() != e[f"{tag}_trellis"]).any(axis=2)
+    same_what = hashlib.sha256(r["W_hat"].contiguous().numpy().tobytes()).digest() == \
+        e[f"{tag}_What_sha256"].tobytes()
+    print(f"{tag}: {int(badm.sum())} tiles differ, W_hat identical {same_what}", flush=True)
+    np.testing.assert_array_equal(r["suh"].float().numpy(), e[f"{tag}_suh"])
+    np.testing.assert_array_equal(r["svh"].float().numpy(), e[f"{tag}_svh"])
+    assert np.float32(r["Wscale"]) == e[f"{tag}_Wscale"]
+    if not cs or same_host:
+        assert int(badm.sum()) == 0 and same_what
+    else:
+        assert int(badm.sum()) <= 64 and len(set(np.nonzero(badm)[1].tolist())) <= 2
+
+
+@pytest.mark.parametrize("cs", (False, True))
+def test_reference_arithmetic_equals_cpu_pipeline(xq, cpu8, cs):
+    """A 4096x4096 weight with an AR(1) Gram (65,536 tiles): the GPU pipeline
+    with reference_arithmetic=True equals the reference's arithmetic with all
+    torch work on the CPU (device="cpu") bit for bit -- trellis, W_hat,
+    suh, svh, Wscale -- on the same host."""
+    import workloads as wl
+    w = wl.c2(device="cpu")
+    W, H = w["W"].float(), w["H"]
+    print(f"case c2 device=cpu cs={cs}", flush=True)
+    rc = xq.quantize_linear(W, H, K=4, margin=0, channel_scales=cs, device="cpu")
+    print(f"case c2 device=cuda reference_arithmetic cs={cs}", flush=True)
+    rg = xq.quantize_linear(W.cuda(), H.cuda(), K=4, margin=0, channel_scales=cs,
+                            device="cuda", reference_arithmetic=True)
+    bad = int((rg["trellis"] != rc["trellis"]).any(dim=-1).sum())
+    assert bad == 0, f"{bad} of 65536 tiles differ"
+    for key in ("W_hat", "suh", "svh"):
+        assert torch.equal(rg[key], rc[key]), key
+    assert rg["Wscale"] == rc["Wscale"]
+
+
+@pytest.mark.parametrize("k,n", [(128, 64), (256, 100), (1024, 384), (4096, 4096)])
+def test_hadamard_kernel_matches_cpu(xq, k, n):
+    """The block-128 Hadamard kernel (had_left / had_right on GPU tensors, and
+    the to_inner / from_inner / rotate_hessian built on them) reproduces the
+    reference's torch CPU results bit for bit (quantize.py:134-168)."""
+    g = torch.Generator().manual_seed(k + n)
+    w = torch.randn(k, n, generator=g) * 0.3
+    h = xq.hadamard128(None, torch.float32)
+    hd = xq.hadamard128("cuda", torch.float32)
+    print(f"case had128 {k}x{n}", flush=True)
+    assert torch.equal(xq.had_left(w.cuda(), hd).cpu(), xq.had_left(w, h))
+    if n % 128 == 0:
+        assert torch.equal(xq.had_right(w.cuda(), hd).cpu(), xq.had_right(w, h))
+        suh = xq.sign_vec(k, 3).half()
+        svh = xq.sign_vec(n, 4).half()
+        wi = xq.to_inner(w, suh, svh, h)
+        assert torch.equal(xq.to_inner(w.cuda(), suh.cuda(), svh.cuda(), hd).cpu(), wi)
+        assert torch.equal(xq.from_inner(wi.cuda(), suh.cuda(), svh.cuda(), hd).cpu(),
+                           xq.from_inner(wi, suh, svh, h))
+    if k == n:
+        Hx = w @ w.t() / n
+        assert torch.equal(xq.rotate_hessian(Hx.cuda(), xq.sign_vec(k, 5).cuda(), hd).cpu(),
+                           xq.rotate_hessian(Hx, xq.sign_vec(k, 5), h))
+
+
 def test_quantize_harness_golden(xq, cpu8):
     e = load_golden("e2e_128.npz")
     Wt = torch.from_numpy(e["prep_Wt"])
