@@ -275,13 +275,17 @@ def cpu_baseline_config(kept, total_tiles: int, port_tiles: int = 32):
             {"blocks_checked": len(kept), "tiles_checked": checked, "tiles_exact": exact})
 
 
+REF_ARITH = False      # --reference-arithmetic: the configs' host-side reductions and factor
+
+
 def _quantize_timed(Ws, H, K, cs, keep=2):
     """quantize_linear_group of the weights Ws (one weight: quantize_linear)
     timed on the wall clock, with the encode sample captured."""
     torch.cuda.synchronize()
     with _LaunchCapture(keep) as cap:
         t0 = time.perf_counter()
-        rs = xq.quantize_linear_group(Ws, H, K=K, device="cuda", margin=0, channel_scales=cs)
+        rs = xq.quantize_linear_group(Ws, H, K=K, device="cuda", margin=0, channel_scales=cs,
+                                      reference_arithmetic=REF_ARITH)
         torch.cuda.synchronize()
         dt = time.perf_counter() - t0
     return rs, dt, cap
@@ -417,6 +421,10 @@ def main():
                     help="bits per weight of the timed steps (profiling; the metric is K=4)")
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-k-sweep", action="store_true", help="skip the K = 2..7 sweep")
+    ap.add_argument("--reference-arithmetic", action="store_true",
+                    help="configs: quantize_linear(reference_arithmetic=True) -- reductions and "
+                         "the block-LDL factorisation on the host CPU, bit-identical to the "
+                         "reference's device='cpu' result")
     ap.add_argument("--no-full-check", action="store_true",
                     help="skip checking every tile against the reference's torch Viterbi "
                          "run on the GPU")
@@ -429,6 +437,8 @@ def main():
                     help="after the timed steps, copy a buffer of BYTES bytes three times "
                          "(a known-traffic kernel for scaling HBM counters)")
     args = ap.parse_args()
+    global REF_ARITH
+    REF_ARITH = bool(args.reference_arithmetic)
     xq.DEFAULT_SCHEDULE = args.schedule
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; multi-GPU runs are out of scope "
@@ -547,6 +557,7 @@ def main():
             torch.cuda.empty_cache()
             log(f"end-to-end configs {names} ...")
             result["configs"] = run_configs(names)
+            result["configs"]["reference_arithmetic"] = REF_ARITH
     print(json.dumps(result), flush=True)
 
 
