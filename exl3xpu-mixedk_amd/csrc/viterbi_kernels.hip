@@ -294,6 +294,16 @@ __device__ __forceinline__ void fwd_run(
             // they stay put in VGPRs rather than being re-derived.
 #pragma unroll
             for (int l = 0; l < G::NSTATE; ++l) asm volatile("" : "+v"(f32[l]));
+#ifdef XTQ_REMAT
+            int tl = tid;
+            asm volatile("" : "+v"(tl));
+            const int jb = G::HALF ? (tl >> 1) : tl * G::C;
+            const int wb = G::HALF ? (tl & 1) * G::W : 0;
+            const int ab = jb >> K;
+            const int rp = bslot<K>(ab + wb * G::Q) - (ab + wb * G::Q);
+#else
+            const int tl = tid, jb = jbase, wb = wbase, ab = a0, rp = rpad;
+#endif
             const int q = q0 + tt;
             const float negx = -__int_as_float(
                 __builtin_amdgcn_readfirstlane(__float_as_int(xs[tt][u])));
@@ -306,7 +316,7 @@ __device__ __forceinline__ void fwd_run(
                 float B[G::NB][NCH];
 #pragma unroll
                 for (int w = 0; w < NCH; ++w) {
-                    const float* src = bcur + a0 + rpad + (wbase + qc * NCH + w) * G::Q;
+                    const float* src = bcur + ab + rp + (wb + qc * NCH + w) * G::Q;
                     if constexpr (G::NB == 4) {
                         const float4 v = *(const float4*)src;
                         B[0][w] = v.x; B[1][w] = v.y; B[2][w] = v.z; B[3][w] = v.w;
@@ -382,7 +392,7 @@ __device__ __forceinline__ void fwd_run(
                         // K=3's 8 measured 2 % slower this way)
                         static_assert(NCHUNK == 1 && G::C % 4 == 0, "run[c] final per group");
                         if (c % 4 == 3 && i + 1 < nsteps) {
-                            float* bq = bbuf[tt][(i + 1) & 1] + bslot<K>(jbase) + (c - 3);
+                            float* bq = bbuf[tt][(i + 1) & 1] + bslot<K>(jb) + (c - 3);
                             *(float4*)bq = make_float4(key_cost(run[c - 3]), key_cost(run[c - 2]),
                                                        key_cost(run[c - 1]), key_cost(run[c]));
                         }
@@ -397,7 +407,7 @@ __device__ __forceinline__ void fwd_run(
             gbyte_t* const bprow =
                 uniform_gptr(bp + ((size_t)q * kSlots + (size_t)i) * G::BPSTEP);
             if (i + 1 < nsteps) {
-                float* bnext = bbuf[tt][(i + 1) & 1] + bslot<K>(jbase);
+                float* bnext = bbuf[tt][(i + 1) & 1] + bslot<K>(jb);
                 if constexpr (G::C == 2 || G::C == 4) {
                     lds_store_costs<G::C>(lds_addr(bnext), run);
                 } else if constexpr (K == 2) {
@@ -412,12 +422,12 @@ __device__ __forceinline__ void fwd_run(
                             make_float4(key_cost(run[c]), key_cost(run[c + 1]),
                                         key_cost(run[c + 2]), key_cost(run[c + 3]));
                 } else {
-                    if (!G::HALF || (tid & 1) == 0) bnext[0] = key_cost(run[0]);
+                    if (!G::HALF || (tl & 1) == 0) bnext[0] = key_cost(run[0]);
                 }
                 if (i >= store_lo) {
                     if constexpr (G::HALF) {
-                        if ((tid & 1) == 0)
-                            bprow[(uint32_t)jbase] = (uint8_t)(key_lo(run[0]) & 0x7F);
+                        if ((tl & 1) == 0)
+                            bprow[(uint32_t)jb] = (uint8_t)(key_lo(run[0]) & 0x7F);
                     } else {
                         // Funnel-shift each group's K index bits (the low bits
                         // of its key tag) in from the top, one v_alignbit_b32
@@ -428,7 +438,7 @@ __device__ __forceinline__ void fwd_run(
                         for (int c = 0; c < G::C; ++c)
                             bits = __builtin_amdgcn_alignbit(key_lo(run[c]), bits, (uint32_t)K);
                         if constexpr (G::BITS < 32) bits >>= (32 - G::BITS);
-                        *(__attribute__((address_space(1))) unit_t*)(bprow + (uint32_t)(tid * G::UNIT)) =
+                        *(__attribute__((address_space(1))) unit_t*)(bprow + (uint32_t)(tl * G::UNIT)) =
                             (unit_t)bits;
                     }
                 }
@@ -441,7 +451,7 @@ __device__ __forceinline__ void fwd_run(
                 const int ov = ovs[tt];
 #pragma unroll
                 for (int c = 0; c < G::C; ++c)
-                    if (jbase + c == ov && (!G::HALF || (tid & 1) == 0)) {
+                    if (jb + c == ov && (!G::HALF || (tl & 1) == 0)) {
                         const float m = key_cost(run[c]);
                         send[tt] = (m == __builtin_inff())
                                       ? 0
@@ -454,7 +464,7 @@ __device__ __forceinline__ void fwd_run(
                 double best = 0.0;
 #pragma unroll
                 for (int c = 0; c < G::C; ++c) {
-                    const uint32_t s = (uint32_t)(jbase + c) +
+                    const uint32_t s = (uint32_t)(jb + c) +
                                        (key_lo(run[c]) & (uint32_t)(G::NC - 1)) * (uint32_t)G::SP;
                     const double kc = key_of(s, key_cost(run[c]));
                     best = (c == 0) ? kc : kmin(best, kc);
