@@ -207,6 +207,14 @@ constexpr int kChunkW =
 template <int K>
 constexpr int kPrioTop = K == 3 ? 1 : 2;
 
+// Whether a sequence-step recomputes the lane's offsets instead of keeping
+// them live (see fwd_run): measured faster for one sequence per workgroup
+// at K = 2, 3 (the column chain: 5120x5120 sweep K=2 -3 %, K=3 -6 %; K=2
+// batched unchanged) and slower elsewhere (batched K=5..7 -1..-4 %, the
+// chain at K=4 +1.5 %).
+template <int K, int T>
+constexpr bool kRematLane = (T == 1 && K <= 3);
+
 // Shared memory of one forward run over T sequences.
 template <int K, int T>
 struct FwdSmem {
@@ -294,16 +302,19 @@ __device__ __forceinline__ void fwd_run(
             // they stay put in VGPRs rather than being re-derived.
 #pragma unroll
             for (int l = 0; l < G::NSTATE; ++l) asm volatile("" : "+v"(f32[l]));
-#ifdef XTQ_REMAT
-            int tl = tid;
-            asm volatile("" : "+v"(tl));
-            const int jb = G::HALF ? (tl >> 1) : tl * G::C;
-            const int wb = G::HALF ? (tl & 1) * G::W : 0;
-            const int ab = jb >> K;
-            const int rp = bslot<K>(ab + wb * G::Q) - (ab + wb * G::Q);
-#else
-            const int tl = tid, jb = jbase, wb = wbase, ab = a0, rp = rpad;
-#endif
+            // The lane's LDS and backpointer offsets: kept live across the
+            // steps, or (kRematLane) recomputed here from an opaque copy of
+            // the thread index, which frees their registers -- the compiler
+            // had spilled them and reloaded them (a scratch load and a wait)
+            // at every step.
+            int tl = tid, jb = jbase, wb = wbase, ab = a0, rp = rpad;
+            if constexpr (kRematLane<K, T>) {
+                asm volatile("" : "+v"(tl));
+                jb = G::HALF ? (tl >> 1) : tl * G::C;
+                wb = G::HALF ? (tl & 1) * G::W : 0;
+                ab = jb >> K;
+                rp = bslot<K>(ab + wb * G::Q) - (ab + wb * G::Q);
+            }
             const int q = q0 + tt;
             const float negx = -__int_as_float(
                 __builtin_amdgcn_readfirstlane(__float_as_int(xs[tt][u])));
