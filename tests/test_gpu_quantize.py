@@ -184,6 +184,26 @@ def test_reference_arithmetic_equals_cpu_pipeline(xq, cpu8, cs):
     assert rg["Wscale"] == rc["Wscale"]
 
 
+def test_reference_arithmetic_mixed_k_group(xq, cpu8):
+    """quantize_linear_group of q/k/v-like members at K = [5, 7, 7] with
+    channel scales on the GPU under reference_arithmetic (concurrent chain
+    launches per K) equals each member's device="cpu" quantize_linear."""
+    import workloads as wl
+    g = torch.Generator().manual_seed(31)
+    H = wl.ar1_gram(512, 1024, 0.5, 31)
+    Ws = [0.02 * torch.randn(512, 512, generator=g), 0.03 * torch.randn(128, 512, generator=g),
+          0.02 * torch.randn(128, 512, generator=g)]
+    Ks = [5, 7, 7]
+    print("case mixed-K group reference_arithmetic on the GPU", flush=True)
+    grp = xq.quantize_linear_group([W.cuda() for W in Ws], H.cuda(), K=Ks, device="cuda",
+                                   channel_scales=True, reference_arithmetic=True)
+    for W, Km, r in zip(Ws, Ks, grp):
+        c = xq.quantize_linear(W, H, K=Km, device="cpu", channel_scales=True)
+        for key in ("trellis", "W_hat", "suh", "svh"):
+            assert torch.equal(r[key], c[key]), (Km, key)
+        assert r["Wscale"] == c["Wscale"]
+
+
 @pytest.mark.parametrize("k,n", [(128, 64), (256, 100), (1024, 384), (4096, 4096)])
 def test_hadamard_kernel_matches_cpu(xq, k, n):
     """The block-128 Hadamard kernel (had_left / had_right on GPU tensors, and
