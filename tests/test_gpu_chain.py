@@ -217,9 +217,11 @@ def test_chain_nan_rejected(hb):
 
 
 def test_chain_vs_block_schedule(xq, monkeypatch):
-    """quantize_linear with the sweep as column chains and as the reference's
-    block schedule: the same encoder on targets that differ only in fp32
-    rounding of the feedback, so the proxy losses agree closely."""
+    """quantize_linear on GPU tensors with the sweep as column chains and as
+    the reference's block schedule, whose feedback then runs as torch GPU
+    GEMMs (rounding unlike the reference's CPU order, which the chain
+    follows): the same encoder on targets that differ by an ulp here and
+    there, so the proxy losses agree closely."""
     import workloads as wl
     g = torch.Generator().manual_seed(11)
     W = 0.02 * torch.randn(256, 512, generator=g)
