@@ -25,6 +25,10 @@ batch), targets resident in HBM before the timed region.  Prints one JSON line:
                and a larger one through the C oracle are checked bit for bit
   bit_exact_pct every tile of the benchmark's output against the same torch
                restatement run on the GPU (and the samples above)
+  host_entry   tiles/s through the reference's host-pointer entry xtq_vit_run
+               (pageable host targets in, states out, PCIe copies included) in
+               calls of 4,096 sequences, every tile compared with the timed
+               steps' output; not the metric
   k_sweep      tiles/s for K = 2..7 on the first 65,536 tiles
   configs      whole-tensor quantize_linear time with BlockLDLQ on the GPU for
                the synthetic workloads c1..c5 (workloads.py; c3 for every K,
@@ -71,6 +75,94 @@ OUT_F, IN_F = 5120, 17408
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
+
+
+_MONITOR_CHILD = r"""
+import json, select, sys, time
+out = {"source": "amdsmi GPU metrics, sampled every 100 ms over the timed steps"}
+try:
+    import amdsmi
+    amdsmi.amdsmi_init()
+    handles = amdsmi.amdsmi_get_processor_handles()
+except Exception as e:
+    handles, out["error"] = [], repr(e)
+cmd = sys.stdin.readline().split()
+h = None
+if len(cmd) == 3 and cmd[0] == "start":
+    for x in handles:
+        dom, bus = amdsmi.amdsmi_get_gpu_device_bdf(x).split(":")[:2]
+        if int(dom, 16) == int(cmd[1]) and int(bus, 16) == int(cmd[2]):
+            h = x
+clk, pw, hot = [], [], []
+while h is not None and not select.select([sys.stdin], [], [], 0.1)[0]:
+    try:
+        m = amdsmi.amdsmi_get_gpu_metrics_info(h)
+    except Exception as e:
+        out["error"] = repr(e)
+        break
+    c = [v for v in m.get("current_gfxclks") or [] if isinstance(v, int) and 0 < v < 65535]
+    if c:
+        clk.append((sum(c) / len(c), min(c)))
+    if isinstance(m.get("current_socket_power"), int):
+        pw.append(m["current_socket_power"])
+    if isinstance(m.get("temperature_hotspot"), int):
+        hot.append(m["temperature_hotspot"])
+if h is None and "error" not in out:
+    out["error"] = "no GPU with the benchmark device's PCI address"
+out["samples"] = len(clk)
+if clk:
+    out["gfxclk_mhz_mean"] = round(sum(a for a, _ in clk) / len(clk))
+    out["gfxclk_mhz_min"] = min(b for _, b in clk)
+if pw:
+    out["socket_power_w_mean"] = round(sum(pw) / len(pw))
+if hot:
+    out["hotspot_c_max"] = max(hot)
+print(json.dumps(out), flush=True)
+"""
+
+
+class DeviceMonitor:
+    """GPU clock, socket power and hotspot temperature over the timed steps,
+    sampled by a child process (amdsmi): the same code runs a few percent
+    slower on a GPU held at lower clocks, and this records which case a run
+    was.  The child starts before this process touches the GPU."""
+
+    def __init__(self, enabled: bool = True):
+        import subprocess
+        self.p = None
+        # not under a profiler, whose preloaded library would start with the child
+        prof = "rocprof" in os.environ.get("LD_PRELOAD", "") or any(
+            k.startswith("ROCPROF") for k in os.environ)
+        if not enabled or prof:
+            return
+        try:
+            self.p = subprocess.Popen([sys.executable, "-c", _MONITOR_CHILD],
+                                      stdin=subprocess.PIPE, stdout=subprocess.PIPE,
+                                      stderr=subprocess.DEVNULL, text=True)
+        except OSError:
+            self.p = None
+
+    def start(self, device=0):
+        if self.p is None:
+            return
+        pr = torch.cuda.get_device_properties(device)
+        try:
+            self.p.stdin.write(f"start {pr.pci_domain_id} {pr.pci_bus_id}\n")
+            self.p.stdin.flush()
+        except OSError:
+            self.p = None
+
+    def stop(self):
+        if self.p is None:
+            return None
+        import subprocess
+        try:
+            out, _ = self.p.communicate("stop\n", timeout=20)
+            return json.loads(out.strip().splitlines()[-1])
+        except (subprocess.TimeoutExpired, ValueError, IndexError, OSError):
+            self.p.kill()
+            self.p.wait()
+            return None
 
 
 def make_targets(seed: int = 4) -> torch.Tensor:
@@ -169,6 +261,43 @@ def full_check(X: torch.Tensor, trellis: torch.Tensor, batch: int = 16384):
             "checker": "the reference's torch tail-bite (oracle/torch_port.py) on the GPU, "
                        f"every tile, {batch} tiles per batch",
             "seconds": round(dt, 1)}
+
+
+def host_entry(X: torch.Tensor, trellis: torch.Tensor, per_call: int = 4096):
+    """The reference's host-pointer boundary, xtq_vit_run (viterbi_esimd.cpp:970;
+    pageable host targets in, host states out, both PCIe copies inside each
+    call), over the whole workload in calls of `per_call` sequences, the
+    reference's default XTQ_VIT_MAXSEQ.  Every tile's states are packed on the
+    GPU and compared with the timed steps' trellis (not timed)."""
+    L = hb.lib()
+    Xh = np.ascontiguousarray(X.cpu().numpy())
+    n = Xh.shape[0]
+    out = np.empty((n, 256), dtype=np.int32)
+    code = b"mul1"
+    rc = L.xtq_vit_run(Xh.ctypes.data, min(per_call, n), code, MARGIN, PIVOT, out.ctypes.data)
+    if rc:
+        raise RuntimeError(f"xtq_vit_run: status {rc}")
+    calls = 0
+    t0 = time.perf_counter()
+    for c0 in range(0, n, per_call):
+        m = min(per_call, n - c0)
+        rc = L.xtq_vit_run(Xh[c0:c0 + m].ctypes.data, m, code, MARGIN, PIVOT,
+                           out[c0:c0 + m].ctypes.data)
+        if rc:
+            raise RuntimeError(f"xtq_vit_run: status {rc}")
+        calls += 1
+    dt = time.perf_counter() - t0
+    bad = 0
+    for c0 in range(0, n, 65536):
+        st = torch.from_numpy(out[c0:c0 + 65536]).to(X.device)
+        bad += int((hb.pack(st, KBITS) != trellis[c0:c0 + 65536]).any(dim=1).sum())
+    torch.cuda.synchronize()
+    return {"value": round(n / dt, 1), "unit": "tiles/s", "calls": calls,
+            "seqs_per_call": per_call, "seconds": round(dt, 3),
+            "pcie_bytes": 2 * n * 256 * 4,
+            "tiles_equal_to_device_entry": n - bad, "tiles": n,
+            "note": "xtq_vit_run on pageable host buffers (targets in, states out), "
+                    "copies included; not the metric, whose inputs are resident in HBM"}
 
 
 def k_sweep(X: torch.Tensor, n: int = 65536):
@@ -421,6 +550,10 @@ def main():
                     help="bits per weight of the timed steps (profiling; the metric is K=4)")
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-k-sweep", action="store_true", help="skip the K = 2..7 sweep")
+    ap.add_argument("--no-monitor", action="store_true",
+                    help="do not sample GPU clocks, power and temperature over the timed steps")
+    ap.add_argument("--no-host-entry", action="store_true",
+                    help="skip timing the host-pointer entry xtq_vit_run (PCIe copies included)")
     ap.add_argument("--reference-arithmetic", action="store_true",
                     help="configs: quantize_linear(reference_arithmetic=True) -- reductions and "
                          "the block-LDL factorisation on the host CPU, bit-identical to the "
@@ -445,6 +578,7 @@ def main():
               "(the encoder shards by output-column tile chains, one process per GPU)",
               file=sys.stderr)
         sys.exit(2)
+    monitor = DeviceMonitor(not args.no_monitor)
     if not torch.cuda.is_available():
         print("bench.py: no HIP device", file=sys.stderr)
         sys.exit(1)
@@ -461,12 +595,14 @@ def main():
         log(f"warmup {w + 1}/{args.warmup} done")
     hb.prof_read()
     hb.prof_enable(True)
+    monitor.start()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for s in range(args.steps):
         tr = run_step(X, args.k)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    device_state = monitor.stop()
     hb.prof_enable(False)
     prof = hb.prof_read()
     log(f"timed {args.steps} steps: {dt:.3f} s")
@@ -531,6 +667,7 @@ def main():
                          "tiles": n, "K": args.k, "pivot": PIVOT, "margin": MARGIN,
                          "codebook": "exl3_mul1"},
               "roofline": roofline,
+              "device_state": device_state,
               "ref_b70_tiles_per_s": REF_B70_TILES_PER_S,
               "speedup_vs_ref_b70": round(tps / REF_B70_TILES_PER_S, 1)}
     if not args.no_extras:
@@ -548,6 +685,10 @@ def main():
             pct = 100.0 * full["tiles_exact"] / full["tiles_checked"]
             result["bit_exact_pct"] = round(min(pct, result.get("bit_exact_pct", 100.0)), 3)
             result.setdefault("bit_exact_tiles", {})["every_tile"] = full
+        if not args.no_host_entry:
+            log("host-pointer entry (xtq_vit_run, PCIe copies included) ...")
+            result["host_entry"] = host_entry(X, tr)
+            log(f"host entry: {result['host_entry']['value']:,.0f} tiles/s")
         if not args.no_k_sweep:
             log("k sweep ...")
             result["k_sweep"] = k_sweep(X)
