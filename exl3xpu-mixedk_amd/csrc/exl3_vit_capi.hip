@@ -421,8 +421,9 @@ bool use_lanes(int n) {
 // Whether a tail-bite at K runs the deferred-argmin forward (group minima
 // rows in HBM, argmin recomputed by the traceback): XTQ_VIT_DEFER=1 for
 // K >= 4, else never.  Measured on the 348,160-tile K=4..7 workloads it is
-// 3-4 % slower end to end: its forward gains 3-9 %, its one-lane
-// tracebacks recomputing NC candidates per link cost more.
+// as fast end to end at K=4 and 2-5 % slower at K=5..7: its forward gains
+// 7-12 %, its one-lane tracebacks recomputing NC candidates per link from
+// scattered minima rows give it back.
 bool use_defer(int K, int nseq) {
     (void)nseq;
     if (K < 4) return false;
