@@ -282,6 +282,18 @@ int grow(P** p, size_t* cap, size_t want, size_t elem, size_t* owned) {
     return 0;
 }
 
+// Releases a buffer whose capacity is tracked in *cap (a failed grow of a
+// group of buffers sharing one capacity leaves them in step again).
+template <typename P>
+void release(P** p, size_t* cap, size_t elem, size_t* owned) {
+    if (*p) {
+        (void)hipFree(*p);
+        *owned -= *cap * elem;
+    }
+    *p = nullptr;
+    *cap = 0;
+}
+
 // K, pivot and margin of a tail-bite call.
 int check_args(int K, int margin, int pivot) {
     if (K < 2 || K > 7) return 9;
@@ -335,15 +347,27 @@ int reserve_scratch(DevCtx& cx, int K, int chunk, bool defer = false) {
         fprintf(stderr, "xtq_vit: request over XTQ_VIT_DEV_MAXBYTES (%zu)\n", g_maxbytes);
         return 5;
     }
+    // (the capacity follows the pointer also when the growth fails: grow
+    // leaves a null pointer and a zero capacity then)
     size_t bpcap_bytes = cx.bp_cap;
-    if (grow((uint8_t**)&cx.bp, &bpcap_bytes, (size_t)chunk * per, 1, &cx.owned)) return 2;
+    const int gb = grow((uint8_t**)&cx.bp, &bpcap_bytes, (size_t)chunk * per, 1, &cx.owned);
     cx.bp_cap = bpcap_bytes;
+    if (gb) return 2;
     size_t sc = cx.seq_cap;
     if ((size_t)chunk > sc) {
+        // send, ov and flags share seq_cap: each keeps its own capacity
+        // while they grow, and a failure releases all three
         size_t sc2 = cx.seq_cap, sc3 = cx.seq_cap;
-        if (grow(&cx.send, &sc, (size_t)chunk, sizeof(int32_t), &cx.owned)) return 2;
-        if (grow(&cx.ov, &sc2, (size_t)chunk, sizeof(int32_t), &cx.owned)) return 2;
-        if (grow(&cx.flags, &sc3, (size_t)chunk, sizeof(uint32_t), &cx.owned)) return 2;
+        int g = grow(&cx.send, &sc, (size_t)chunk, sizeof(int32_t), &cx.owned);
+        if (!g) g = grow(&cx.ov, &sc2, (size_t)chunk, sizeof(int32_t), &cx.owned);
+        if (!g) g = grow(&cx.flags, &sc3, (size_t)chunk, sizeof(uint32_t), &cx.owned);
+        if (g) {
+            release(&cx.send, &sc, sizeof(int32_t), &cx.owned);
+            release(&cx.ov, &sc2, sizeof(int32_t), &cx.owned);
+            release(&cx.flags, &sc3, sizeof(uint32_t), &cx.owned);
+            cx.seq_cap = 0;
+            return 2;
+        }
         // fresh flags hold no epoch of a launch (epochs start at 1)
         if (hipMemset(cx.flags, 0, (size_t)chunk * sizeof(uint32_t)) != hipSuccess) return 4;
         cx.seq_cap = sc;
@@ -714,8 +738,9 @@ int run_ldlq_chain(DevCtx& cx, const float* W, const float* L, int k, int n,
     if (add && hipEventSynchronize(cx.last) != hipSuccess) return 4;
     {
         size_t cap = cx.bp_cap;
-        if (grow((uint8_t**)&cx.bp, &cap, bp_bytes, 1, &cx.owned)) return 2;
+        const int gb = grow((uint8_t**)&cx.bp, &cap, bp_bytes, 1, &cx.owned);
         cx.bp_cap = cap;
+        if (gb) return 2;
     }
     if (grow(&cx.E, &cx.e_cap, need_e, sizeof(float), &cx.owned)) return 2;
     if (grow(&cx.Lt, &cx.lt_cap, need_lt, sizeof(float), &cx.owned)) return 2;
@@ -834,12 +859,16 @@ int run_host(const float* X, int nseq, int K, Code code, int margin, int pivot,
             fprintf(stderr, "xtq_vit: nseq %d over XTQ_VIT_DEV_MAXBYTES\n", nseq);
             rc = 5;
         }
-        size_t c1 = cx.host_cap, c2 = cx.host_cap;
+        // capacities in elements (host_cap counts sequences of kSteps)
+        size_t c1 = cx.host_cap * xtq::kSteps, c2 = c1;
         if (!rc && (size_t)nseq > cx.host_cap && hipEventSynchronize(cx.last) != hipSuccess)
             rc = 4;
         if (!rc && (size_t)nseq > cx.host_cap) {
             if (grow(&cx.hx, &c1, (size_t)nseq * xtq::kSteps, sizeof(float), &cx.owned) ||
                 grow(&cx.hs, &c2, (size_t)nseq * xtq::kSteps, sizeof(int32_t), &cx.owned)) {
+                release(&cx.hx, &c1, sizeof(float), &cx.owned);
+                release(&cx.hs, &c2, sizeof(int32_t), &cx.owned);
+                cx.host_cap = 0;
                 rc = 2;
             } else {
                 cx.host_cap = nseq;
