@@ -336,6 +336,42 @@ def test_chain_edge_shapes(xq, hb, oracle_mod, mul1_lut, k, n, K, pivot, margin)
     _check_tiles(oracle_mod, mul1_lut, K, pivot, margin, st, tr, xt)
 
 
+@pytest.mark.parametrize("buf_cols,K,k,n", [(16, 3, 544, 240), (32, 6, 112, 144),
+                                            (64, 4, 400, 96), (256, 5, 768, 160)])
+def test_chain_buffer_widths(xq, hb, oracle_mod, mul1_lut, cpu8, buf_cols, K, k, n):
+    """Lazy-feedback buffers other than the default 128 columns
+    (quantize.py:631-636 buf_cols).  Up to 128 every tile's targets equal the
+    reference's sweep with the same buffers bit for bit: each buffer's
+    product has an inner dimension of at most 128, one fused multiply-add
+    chain in torch's CPU sgemm.  Wider buffers are summed as one chain each
+    here, while the host BLAS may split inner dimensions above 128 (on the
+    AMD EPYC hosts of the GPU machines it splits 256, on others not), so
+    there the targets are held to the fp64 formula within that order's
+    rounding bound.  The encode of every tile is checked against the oracle
+    either way."""
+    g = torch.Generator().manual_seed(70 + buf_cols)
+    W = torch.randn(k, n, generator=g)
+    L = _lfac(xq, k, buf_cols)
+    perm = xq.tensor_core_perm()
+    print(f"case chain buf_cols={buf_cols} K={K} {k}x{n}", flush=True)
+    hatW, st, tr, xt = (t.cpu() for t in hb.ldlq_chain(W.cuda(), L.cuda(), K, 128, 0,
+                                                        targets=True, buf_cols=buf_cols))
+    if buf_cols <= 128:
+        assert torch.equal(xt, _ref_targets(W, L, hatW, perm, buf_cols=buf_cols))
+    W64, E = W.double(), (W - hatW).double()
+    X64, B = W64.clone(), W64.abs()
+    L64 = L.double()
+    for i in range(k // 16 - 1):
+        r0, r1 = 16 * i, 16 * (i + 1)
+        X64[r0:r1] += L64[r1:, r0:r1].t() @ E[r1:]
+        B[r0:r1] += L64[r1:, r0:r1].abs().t() @ E[r1:].abs()
+    d = (xt.double() - _seq_order(X64, perm)).abs()
+    lim = (buf_cols + k / buf_cols + 3) * U32 * _seq_order(B, perm)
+    assert (d <= lim).all(), f"worst excess {float((d - lim).max()):.3e}"
+    _check_tiles(oracle_mod, mul1_lut, K, 128, 0, st, tr, xt)
+    np.testing.assert_array_equal(hatW.numpy(), oracle_mod.decode(tr.numpy(), mul1_lut, K))
+
+
 def test_chain_many_groups(hb):
     """Four column groups (one narrower than its share of the CUs) equal
     single-K launches over their columns."""
