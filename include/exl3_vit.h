@@ -174,7 +174,9 @@ XTQ_API int xtq_vit_status_dev(void* stream);
  * GEMMs evaluated as torch's CPU sgemm does: one fp32 fused multiply-add
  * chain per output over the rows of each buffer, buffers added in sweep
  * order), so the targets, and hence W_hat and the trellis, equal the
- * reference's ldlq_viterbi on the same W and L.  Synchronous on return.
+ * reference's ldlq_viterbi on the same W and L for buf_cols up to 128 (a
+ * wider buffer is one chain here too, while the host BLAS may split that
+ * inner dimension).  Synchronous on return.
  *   d_W       [k][n] fp32 device, inner domain (k, n multiples of 16)
  *   d_L       [k][k] fp32 device block-LDL factor (row-major, 16-byte
  *             aligned), or NULL for no feedback
