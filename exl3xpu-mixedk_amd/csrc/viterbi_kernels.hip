@@ -152,6 +152,50 @@ __device__ __forceinline__ void lds_store_costs(uint32_t addr, const double* run
     }
 }
 
+// fp32 minima for the steps and kernels that need no argmin.  Costs are never
+// NaN (a NaN target ends the call with status 11) and IEEE min needs no
+// canonicalisation here, so the instructions are issued directly.
+__device__ __forceinline__ float fmin2(float a, float b) {
+    float r;
+    asm("v_min_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+__device__ __forceinline__ float fmin3(float a, float b, float c) {
+    float r;
+    asm("v_min3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
+// Minimum of v[0..N) in triples (a v_min_f32 pair tree measured 3-7 %
+// slower); a level's one or two leftover values pass to the next level
+// unreduced, so N values take ceil((N-1)/2) instructions.
+template <int N>
+__device__ __forceinline__ float fmin_tree(const float* v) {
+    if constexpr (N == 1) {
+        return v[0];
+    } else if constexpr (N == 2) {
+        return fmin2(v[0], v[1]);
+    } else if constexpr (N == 3) {
+        return fmin3(v[0], v[1], v[2]);
+    } else {
+        constexpr int M = N / 3, R = N % 3;
+        float r[M + R];
+#pragma unroll
+        for (int m = 0; m < M; ++m) r[m] = fmin3(v[3 * m], v[3 * m + 1], v[3 * m + 2]);
+#pragma unroll
+        for (int m = 0; m < R; ++m) r[M + m] = v[3 * M + m];
+        return fmin_tree<M + R>(r);
+    }
+}
+
+// A compile-time switch passed to a generic lambda, and the running minimum's
+// type per reduction: a (cost, index) key or the fp32 cost alone.
+template <bool B> struct BoolC { static constexpr bool value = B; };
+template <bool KEYS> struct RunType { typedef float type; };
+template <> struct RunType<true> { typedef double type; };
+__device__ __forceinline__ float cost_of(double k) { return key_cost(k); }
+__device__ __forceinline__ float cost_of(float c) { return c; }
+
 // Backpointer of group j in one step's row.
 template <int K>
 __device__ __forceinline__ int bp_lookup(const uint8_t* row, int j) {
@@ -293,7 +337,20 @@ __device__ __forceinline__ void fwd_run(
     const int a0 = jbase >> K;  // first NC x NC block this thread reads
     // b slot offset of every predecessor this lane reads (constant per lane)
     const int rpad = bslot<K>(a0 + wbase * G::Q) - (a0 + wbase * G::Q);
-    for (int i = 0; i < nsteps; ++i) {
+
+    // Step i of every sequence of the group, then the barrier that publishes
+    // b_{i+1}.  KEYS selects the reduction: steps whose backpointer row is
+    // kept (i >= store_lo) and the last step reduce (cost, index) keys with
+    // v_min_f64; the steps before store_lo, whose links no traceback ever
+    // reads (a run keeps links only after back_from, quantize.py:273-277,
+    // 287-292), reduce the fp32 costs alone with a v_min3_f32 tree -- the
+    // same minima b (the min of a set of non-NaN costs is one of them,
+    // whatever the order), half an instruction per candidate against the
+    // key path's one v_min_f64 (a slow-rate instruction), and no backpointer
+    // row.
+    auto step = [&](auto keys_c, int i) __attribute__((always_inline)) {
+        constexpr bool KEYS = decltype(keys_c)::value;
+        typedef typename RunType<KEYS>::type run_t;
         // Target of step i of the sequence rolled right by `roll`.
         const int u = (i - roll < 0) ? i - roll + xlen : i - roll;
 #pragma unroll 1
@@ -321,7 +378,7 @@ __device__ __forceinline__ void fwd_run(
             if constexpr (K == 2) __builtin_amdgcn_s_setprio(1);
             const float* bcur = bbuf[tt][i & 1];
 
-            double run[G::C];
+            run_t run[G::C];
 #pragma unroll
             for (int qc = 0; qc < NCHUNK; ++qc) {
                 float B[G::NB][NCH];
@@ -353,7 +410,8 @@ __device__ __forceinline__ void fwd_run(
                         }
                         if (pos == D0) __builtin_amdgcn_s_setprio(0);
                     }
-                    double kk[NCH];
+                    // candidate costs fl(fl(fl(f - x)^2) + b)
+                    float dv[NCH];
                     if constexpr (kGroupOps<K, T>) {
                         // Issue the chunk's candidates opcode by opcode (all
                         // subs, then all squares, then all adds): gfx950
@@ -361,7 +419,6 @@ __device__ __forceinline__ void fwd_run(
                         // faster than one per 4 cycles, which a
                         // dependency-ordered schedule forfeits; the empty asm
                         // statements fix the phase order.
-                        float dv[NCH];
 #pragma unroll
                         for (int w = 0; w < NCH; ++w) {
                             dv[w] = fsub(c * G::W + qc * NCH + w, negx);
@@ -373,8 +430,7 @@ __device__ __forceinline__ void fwd_run(
 #pragma unroll
                         for (int w = 0; w < NCH; ++w) asm volatile("" : "+v"(dv[w]));
 #pragma unroll
-                        for (int w = 0; w < NCH; ++w)
-                            kk[w] = key_of(tag[w], dv[w] + B[blk][w]);
+                        for (int w = 0; w < NCH; ++w) dv[w] = dv[w] + B[blk][w];
                     } else {
                         // K <= 3, and K = 4, 5 at T = 1: the compiler's own
                         // interleaving measures faster.
@@ -382,19 +438,33 @@ __device__ __forceinline__ void fwd_run(
                         for (int w = 0; w < NCH; ++w) {
                             const float d = fsub(c * G::W + qc * NCH + w, negx);
                             const float e = d * d;
-                            kk[w] = key_of(tag[w], e + B[blk][w]);
+                            dv[w] = e + B[blk][w];
                         }
                     }
+                    if constexpr (KEYS) {
+                        double kk[NCH];
 #pragma unroll
-                    for (int st = 1; st < NCH; st *= 2)
+                        for (int w = 0; w < NCH; ++w) kk[w] = key_of(tag[w], dv[w]);
 #pragma unroll
-                        for (int w = 0; w < NCH; w += 2 * st) kk[w] = kmin(kk[w], kk[w + st]);
-                    if (qc == 0) {
-                        run[c] = kk[0];
+                        for (int st = 1; st < NCH; st *= 2)
+#pragma unroll
+                            for (int w = 0; w < NCH; w += 2 * st) kk[w] = kmin(kk[w], kk[w + st]);
+                        if (qc == 0) {
+                            run[c] = kk[0];
+                        } else {
+                            const double kq = key_of(key_lo(kk[0]) + (uint32_t)(qc * NCH),
+                                                     key_cost(kk[0]));
+                            run[c] = kmin(run[c], kq);
+                        }
+                    } else if (qc == 0) {
+                        run[c] = fmin_tree<NCH>(dv);
                     } else {
-                        const double kq = key_of(key_lo(kk[0]) + (uint32_t)(qc * NCH),
-                                                 key_cost(kk[0]));
-                        run[c] = kmin(run[c], kq);
+                        // the running minimum joins the chunk's tree
+                        float v[NCH + 1];
+#pragma unroll
+                        for (int w = 0; w < NCH; ++w) v[w] = dv[w];
+                        v[NCH] = run[c];
+                        run[c] = fmin_tree<NCH + 1>(v);
                     }
                     if constexpr (K == 2) {
                         // K=2's 16 costs per lane leave in 16-byte quads as
@@ -404,93 +474,113 @@ __device__ __forceinline__ void fwd_run(
                         static_assert(NCHUNK == 1 && G::C % 4 == 0, "run[c] final per group");
                         if (c % 4 == 3 && i + 1 < nsteps) {
                             float* bq = bbuf[tt][(i + 1) & 1] + bslot<K>(jb) + (c - 3);
-                            *(float4*)bq = make_float4(key_cost(run[c - 3]), key_cost(run[c - 2]),
-                                                       key_cost(run[c - 1]), key_cost(run[c]));
+                            *(float4*)bq = make_float4(cost_of(run[c - 3]), cost_of(run[c - 2]),
+                                                       cost_of(run[c - 1]), cost_of(run[c]));
                         }
                     }
                 }
             }
-            if constexpr (G::HALF) run[0] = kmin_xor1(run[0]);  // merge the two halves
+            if constexpr (G::HALF) {
+                // merge the two halves of the group (lanes 2t, 2t+1)
+                if constexpr (KEYS) {
+                    run[0] = kmin_xor1(run[0]);
+                } else {
+                    const float o = __int_as_float(__builtin_amdgcn_mov_dpp(
+                        __float_as_int(run[0]), 0xB1, 0xF, 0xF, false));
+                    run[0] = fmin2(run[0], o);
+                }
+            }
 
-            // this step's backpointer row: a wave-uniform base (SGPRs) plus a
-            // 32-bit lane offset, so the store takes the SGPR-base form and
-            // no 64-bit per-lane address is carried across steps
-            gbyte_t* const bprow =
-                uniform_gptr(bp + ((size_t)q * kSlots + (size_t)i) * G::BPSTEP);
             if (i + 1 < nsteps) {
                 float* bnext = bbuf[tt][(i + 1) & 1] + bslot<K>(jb);
-                if constexpr (G::C == 2 || G::C == 4) {
-                    lds_store_costs<G::C>(lds_addr(bnext), run);
-                } else if constexpr (K == 2) {
+                if constexpr (K == 2) {
                     // stored per quad of groups above
+                } else if constexpr (KEYS && (G::C == 2 || G::C == 4)) {
+                    lds_store_costs<G::C>(lds_addr(bnext), run);
+                } else if constexpr (G::C == 2) {
+                    *(float2*)bnext = make_float2(cost_of(run[0]), cost_of(run[1]));
                 } else if constexpr (G::C % 4 == 0) {
-                    // 8 or 16 costs per lane: 16-byte stores keep each lane's
-                    // bytes contiguous (dword pairs at a 32/64-byte lane
-                    // stride would pile onto a few LDS banks).
+                    // 4, 8 or 16 costs per lane: 16-byte stores keep each
+                    // lane's bytes contiguous (dword pairs at a 32/64-byte
+                    // lane stride would pile onto a few LDS banks).
 #pragma unroll
                     for (int c = 0; c < G::C; c += 4)
                         *(float4*)(bnext + c) =
-                            make_float4(key_cost(run[c]), key_cost(run[c + 1]),
-                                        key_cost(run[c + 2]), key_cost(run[c + 3]));
+                            make_float4(cost_of(run[c]), cost_of(run[c + 1]),
+                                        cost_of(run[c + 2]), cost_of(run[c + 3]));
                 } else {
-                    if (!G::HALF || (tl & 1) == 0) bnext[0] = key_cost(run[0]);
+                    if (!G::HALF || (tl & 1) == 0) bnext[0] = cost_of(run[0]);
                 }
-                if (i >= store_lo) {
-                    if constexpr (G::HALF) {
-                        if ((tl & 1) == 0)
-                            bprow[(uint32_t)jb] = (uint8_t)(key_lo(run[0]) & 0x7F);
-                    } else {
-                        // Funnel-shift each group's K index bits (the low bits
-                        // of its key tag) in from the top, one v_alignbit_b32
-                        // per group; group c ends at bits [cK, (c+1)K).
-                        typedef typename UnitT<G::UNIT>::type unit_t;
-                        uint32_t bits = 0;
+                if constexpr (KEYS) {
+                    if (i >= store_lo) {
+                        // this step's backpointer row: a wave-uniform base
+                        // (SGPRs) plus a 32-bit lane offset, so the store
+                        // takes the SGPR-base form and no 64-bit per-lane
+                        // address is carried across steps
+                        gbyte_t* const bprow =
+                            uniform_gptr(bp + ((size_t)q * kSlots + (size_t)i) * G::BPSTEP);
+                        if constexpr (G::HALF) {
+                            if ((tl & 1) == 0)
+                                bprow[(uint32_t)jb] = (uint8_t)(key_lo(run[0]) & 0x7F);
+                        } else {
+                            // Funnel-shift each group's K index bits (the low
+                            // bits of its key tag) in from the top, one
+                            // v_alignbit_b32 per group; group c ends at bits
+                            // [cK, (c+1)K).
+                            typedef typename UnitT<G::UNIT>::type unit_t;
+                            uint32_t bits = 0;
 #pragma unroll
-                        for (int c = 0; c < G::C; ++c)
-                            bits = __builtin_amdgcn_alignbit(key_lo(run[c]), bits, (uint32_t)K);
-                        if constexpr (G::BITS < 32) bits >>= (32 - G::BITS);
-                        *(__attribute__((address_space(1))) unit_t*)(bprow + (uint32_t)(tl * G::UNIT)) =
-                            (unit_t)bits;
+                            for (int c = 0; c < G::C; ++c)
+                                bits = __builtin_amdgcn_alignbit(key_lo(run[c]), bits, (uint32_t)K);
+                            if constexpr (G::BITS < 32) bits >>= (32 - G::BITS);
+                            *(__attribute__((address_space(1))) unit_t*)(bprow +
+                                                                         (uint32_t)(tl * G::UNIT)) =
+                                (unit_t)bits;
+                        }
                     }
                 }
-            } else if (pinned) {
-                // Pinned end: the allowed final states are exactly group ov's
-                // candidates, so s_end = ov + argmin_w * SP.  When even the
-                // best allowed cost is +inf, cost + mask is +inf everywhere
-                // and the reference's argmin returns state 0
-                // (quantize.py:298-306).
-                const int ov = ovs[tt];
+            } else if constexpr (KEYS) {
+                if (pinned) {
+                    // Pinned end: the allowed final states are exactly group
+                    // ov's candidates, so s_end = ov + argmin_w * SP.  When
+                    // even the best allowed cost is +inf, cost + mask is +inf
+                    // everywhere and the reference's argmin returns state 0
+                    // (quantize.py:298-306).
+                    const int ov = ovs[tt];
 #pragma unroll
-                for (int c = 0; c < G::C; ++c)
-                    if (jb + c == ov && (!G::HALF || (tl & 1) == 0)) {
-                        const float m = key_cost(run[c]);
-                        send[tt] = (m == __builtin_inff())
-                                      ? 0
-                                      : ov + (int)(key_lo(run[c]) & (uint32_t)(G::NC - 1)) * G::SP;
+                    for (int c = 0; c < G::C; ++c)
+                        if (jb + c == ov && (!G::HALF || (tl & 1) == 0)) {
+                            const float m = key_cost(run[c]);
+                            send[tt] = (m == __builtin_inff())
+                                          ? 0
+                                          : ov + (int)(key_lo(run[c]) & (uint32_t)(G::NC - 1)) *
+                                                     G::SP;
+                        }
+                } else {
+                    // Free end: lowest state index among the minimum costs.
+                    // The first argmin of a group is its lowest state; across
+                    // groups compare (cost, state) as one key.
+                    double best = 0.0;
+#pragma unroll
+                    for (int c = 0; c < G::C; ++c) {
+                        const uint32_t s = (uint32_t)(jb + c) +
+                                           (key_lo(run[c]) & (uint32_t)(G::NC - 1)) *
+                                               (uint32_t)G::SP;
+                        const double kc = key_of(s, key_cost(run[c]));
+                        best = (c == 0) ? kc : kmin(best, kc);
                     }
-            } else {
-                // Free end: lowest state index among the minimum costs.  The
-                // first argmin of a group is its lowest state; across groups
-                // compare (cost, state) as one key.
-                double best = 0.0;
 #pragma unroll
-                for (int c = 0; c < G::C; ++c) {
-                    const uint32_t s = (uint32_t)(jb + c) +
-                                       (key_lo(run[c]) & (uint32_t)(G::NC - 1)) * (uint32_t)G::SP;
-                    const double kc = key_of(s, key_cost(run[c]));
-                    best = (c == 0) ? kc : kmin(best, kc);
+                    for (int m = 32; m >= 1; m >>= 1) best = kmin_xor(best, m);
+                    if ((tid & 63) == 0) red[tid >> 6] = best;
+                    __syncthreads();
+                    if (tid == 0) {
+                        double b = red[0];
+#pragma unroll
+                        for (int wv = 1; wv < kFwdThreads / 64; ++wv) b = kmin(b, red[wv]);
+                        send[tt] = (int)key_lo(b);
+                    }
+                    __syncthreads();
                 }
-#pragma unroll
-                for (int m = 32; m >= 1; m >>= 1) best = kmin_xor(best, m);
-                if ((tid & 63) == 0) red[tid >> 6] = best;
-                __syncthreads();
-                if (tid == 0) {
-                    double b = red[0];
-#pragma unroll
-                    for (int wv = 1; wv < kFwdThreads / 64; ++wv) b = kmin(b, red[wv]);
-                    send[tt] = (int)key_lo(b);
-                }
-                __syncthreads();
             }
         }
         // The cost stores above are inline ds_write2_b32 the compiler does
@@ -498,7 +588,14 @@ __device__ __forceinline__ void fwd_run(
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __syncthreads();
         __builtin_amdgcn_s_setprio(kPrioTop<K>);
-    }
+    };
+
+    // Min-only steps 0 .. npre-1 (never the last step, which takes the
+    // final argmin), then the key steps.
+    const int npre = store_lo <= 0 ? 0 : (store_lo < nsteps - 1 ? store_lo : nsteps - 1);
+    int i = 0;
+    for (; i < npre; ++i) step(BoolC<false>{}, i);
+    for (; i < nsteps; ++i) step(BoolC<true>{}, i);
     __builtin_amdgcn_s_setprio(0);
 }
 
@@ -773,41 +870,6 @@ __global__ __launch_bounds__(kTbLaneSeqs) void tb_lane_kernel(
 // tile-step is 16 KiB at K=4 (8 times the packed backpointers) and 2 KiB at
 // K=7; K = 2, 3 would write 64 / 32 KiB per tile-step, more than HBM takes at
 // the forward's rate, so they keep fwd_run.
-__device__ __forceinline__ float fmin2(float a, float b) {
-    float r;
-    asm("v_min_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-    return r;
-}
-__device__ __forceinline__ float fmin3(float a, float b, float c) {
-    float r;
-    asm("v_min3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
-}
-
-// Minimum of v[0..N) (costs are never NaN: a NaN target ends the call with
-// status 11, and IEEE min needs no canonicalisation here), in triples
-// (a v_min_f32 pair tree measured 3-7 % slower).
-template <int N>
-__device__ __forceinline__ float min_tree(const float* v) {
-    if constexpr (N == 1) {
-        return v[0];
-    } else if constexpr (N == 2) {
-        return fmin2(v[0], v[1]);
-    } else if constexpr (N == 3) {
-        return fmin3(v[0], v[1], v[2]);
-    } else {
-        constexpr int M = (N + 2) / 3;
-        float r[M];
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-            if (3 * m + 2 < N) r[m] = fmin3(v[3 * m], v[3 * m + 1], v[3 * m + 2]);
-            else if (3 * m + 1 < N) r[m] = fmin2(v[3 * m], v[3 * m + 1]);
-            else r[m] = v[3 * m];
-        }
-        return min_tree<M>(r);
-    }
-}
-
 // Minima rows kept per sequence (row r holds b_r, r = 1 .. 254) and their
 // bytes per sequence.
 template <int K>
@@ -920,7 +982,7 @@ __device__ __forceinline__ void fwd_run_defer(
                             dv[w] = d * d + B[0][w];
                         }
                     }
-                    const float m = min_tree<NCH>(dv);
+                    const float m = fmin_tree<NCH>(dv);
                     run[c] = (qc == 0) ? m : fmin2(run[c], m);
                 }
             }
