@@ -989,6 +989,19 @@ int xtq_vit_tailbite_dev_noalloc(const float* dX, int nseq, int K, const char* c
     if (nseq <= 0) return 6;
     rc = check_args(K, margin, pivot);
     if (rc) return rc;
+    // Synchronous (it reads its status word back and waits for the stream),
+    // so it refuses a stream under graph capture rather than invalidate the
+    // caller's capture with a copy to the host and a synchronisation.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing((hipStream_t)stream, &cs) != hipSuccess) {
+        fprintf(stderr, "xtq_vit run: %s\n", hipGetErrorString(hipGetLastError()));
+        return 4;
+    }
+    if (cs != hipStreamCaptureStatusNone) {
+        fprintf(stderr, "xtq_vit: xtq_vit_tailbite_dev_noalloc is synchronous and cannot run on "
+                "a stream under graph capture\n");
+        return 13;
+    }
     int dev = 0;
     if (current_device(&dev)) return 1;
     // Setting a device up allocates (codebook tables, status words): that is
@@ -1123,12 +1136,12 @@ int xtq_trellis_unpack_dev(const int16_t* d_trellis, int nt, int K, int32_t* d_s
     return 0;
 }
 
-int xtq_had128_left_dev(const float* d_h, const float* d_in, float* d_out, int rows, int cols,
+int xtq_had128_left_dev(const float* d_ht, const float* d_in, float* d_out, int rows, int cols,
                         void* stream) {
-    if (!d_h || !d_in || !d_out) return 12;
+    if (!d_ht || !d_in || !d_out) return 12;
     if (d_in == d_out) return 12;
     if (rows <= 0 || cols <= 0 || rows % 128 || rows / 128 > 65535) return 6;
-    hipError_t e = xtq::launch_had_left(d_h, d_in, d_out, rows, cols, (hipStream_t)stream);
+    hipError_t e = xtq::launch_had_left(d_ht, d_in, d_out, rows, cols, (hipStream_t)stream);
     if (e != hipSuccess) {
         fprintf(stderr, "xtq_vit had128: %s\n", hipGetErrorString(e));
         return 4;
@@ -1200,6 +1213,7 @@ const char* xtq_vit_strerror(int rc) {
         case 10: return "pivot or margin out of range";
         case 11: return "NaN target";
         case 12: return "null or misaligned pointer argument";
+        case 13: return "synchronous entry given a stream under graph capture";
         default: return "unknown status";
     }
 }

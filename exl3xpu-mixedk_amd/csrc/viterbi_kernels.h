@@ -90,10 +90,10 @@ hipError_t launch_tailbite_fused(int K, const float* X, int nseq, const uint16_t
 // lfac_quads_kernel; only the part below the diagonal blocks).
 hipError_t launch_lfac_quads(const float* L, int k, float* Lq, hipStream_t stream);
 
-// out = blockdiag(h) @ in for in, out [rows][cols] fp32 row-major (rows a
-// multiple of 128, in != out), h the [128][128] normalised Sylvester matrix:
-// each output one fp32 fused multiply-add chain in ascending order.
-hipError_t launch_had_left(const float* h, const float* in, float* out, int rows, int cols,
+// out = blockdiag(ht^T) @ in for in, out [rows][cols] fp32 row-major (rows a
+// multiple of 128, in != out), ht[t][r] the weight of input row t in output
+// row r: each output one fp32 fused multiply-add chain in ascending order.
+hipError_t launch_had_left(const float* ht, const float* in, float* out, int rows, int cols,
                            hipStream_t stream);
 
 // The BlockLDLQ sweep of the column tiles jc0 .. jc0+tnl-1 of W [k][n]

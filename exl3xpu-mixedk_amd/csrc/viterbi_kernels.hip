@@ -1382,14 +1382,14 @@ __global__ __launch_bounds__(256) void lfac_quads_kernel(const float* __restrict
 }
 
 // ------------------------------------------------- block-128 Hadamard
-// out[128b + r][c] = sum_{t=0..127} h[r][t] * in[128b + t][c] (had_left,
-// quantize.py:134-138), evaluated as torch's CPU sgemm evaluates it: one
-// fp32 fused multiply-add chain per output over t ascending, from zero
-// (measured bit for bit against an fmaf chain).  h is the caller's
-// normalised Sylvester matrix, which is symmetric, so h[r][t] = h[t][r] and
-// the 16 multipliers a wave needs at step t are one contiguous, wave-uniform
-// row segment (scalar loads).  Wave: 16 rows x 64 columns; workgroup: 4 waves.
-__global__ __launch_bounds__(256) void had_left_kernel(const float* __restrict__ h,
+// out[128b + r][c] = sum_{t=0..127} ht[t][r] * in[128b + t][c] (had_left,
+// quantize.py:134-138, with ht = h^T: the multipliers by input row),
+// evaluated as torch's CPU sgemm evaluates it: one fp32 fused multiply-add
+// chain per output over t ascending, from zero (measured bit for bit against
+// an fmaf chain).  Taking h^T makes the 16 multipliers a wave needs at step t
+// one contiguous, wave-uniform row segment (scalar loads).  Wave: 16 rows x
+// 64 columns; workgroup: 4 waves.
+__global__ __launch_bounds__(256) void had_left_kernel(const float* __restrict__ ht,
                                                        const float* __restrict__ in,
                                                        float* __restrict__ out, int cols) {
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), ln = threadIdx.x & 63;
@@ -1402,7 +1402,7 @@ __global__ __launch_bounds__(256) void had_left_kernel(const float* __restrict__
     for (int q = 0; q < 16; ++q) acc[q] = 0.0f;
     for (int t = 0; t < 128; ++t) {
         const float w = src[(size_t)t * cols];
-        const float* hr = h + t * 128 + r0;
+        const float* hr = ht + t * 128 + r0;
 #pragma unroll
         for (int q = 0; q < 16; ++q) acc[q] = __builtin_fmaf(hr[q], w, acc[q]);
     }
@@ -1898,12 +1898,12 @@ hipError_t launch_tailbite_fused(int K, const float* X, int nseq, const uint16_t
                               epoch, spin_limit, err, stream);
 }
 
-hipError_t launch_had_left(const float* h, const float* in, float* out, int rows, int cols,
+hipError_t launch_had_left(const float* ht, const float* in, float* out, int rows, int cols,
                            hipStream_t stream) {
     if (rows <= 0 || cols <= 0) return hipSuccess;
     if (rows % 128 || rows / 128 > 65535) return hipErrorInvalidValue;
     hipLaunchKernelGGL(had_left_kernel, dim3((cols + 63) / 64, rows / 128, 2), dim3(256), 0,
-                       stream, h, in, out, cols);
+                       stream, ht, in, out, cols);
     return hipGetLastError();
 }
 

@@ -253,10 +253,11 @@ def decode(trellis: torch.Tensor, K: int, code: str = "mul1",
 
 
 def had128_left(w: torch.Tensor, h: torch.Tensor) -> torch.Tensor:
-    """blockdiag(h) @ w for w [k, n] fp32 (device, k a multiple of 128), h
-    the normalised 128x128 Sylvester matrix on the same device: each output
-    one fused multiply-add chain in ascending order, as torch's CPU sgemm
-    evaluates the reference's matmul (xtq_had128_left_dev)."""
+    """blockdiag(h) @ w for w [k, n] fp32 (device, k a multiple of 128) and
+    any 128x128 h on the same device (the reference applies the normalised
+    Sylvester matrix): each output one fused multiply-add chain in ascending
+    order, as torch's CPU sgemm evaluates the reference's matmul
+    (xtq_had128_left_dev, which takes the multipliers by input row, h^T)."""
     w = _dev_tensor(w, torch.float32, "w")
     h = _dev_tensor(h, torch.float32, "h")
     if w.dim() != 2 or w.shape[0] % 128 or h.shape != (128, 128) or h.device != w.device:
@@ -266,7 +267,8 @@ def had128_left(w: torch.Tensor, h: torch.Tensor) -> torch.Tensor:
     if w.numel() == 0:
         return out
     with torch.cuda.device(w.device):
-        rc = lib().xtq_had128_left_dev(h.data_ptr(), w.data_ptr(), out.data_ptr(), w.shape[0],
+        ht = h.t().contiguous()
+        rc = lib().xtq_had128_left_dev(ht.data_ptr(), w.data_ptr(), out.data_ptr(), w.shape[0],
                                        w.shape[1], _stream(w.device))
     _check("xtq_had128_left_dev", rc)
     return out

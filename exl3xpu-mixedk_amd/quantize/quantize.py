@@ -139,18 +139,19 @@ def had_left(w: torch.Tensor, h: torch.Tensor) -> torch.Tensor:
     k, n = w.shape
     assert k % 128 == 0
     if w.is_cuda and w.dtype == torch.float32:
-        return _hb.had128_left(w.contiguous(), h.to(w.device, torch.float32).contiguous())
+        return _hb.had128_left(w.contiguous(), h.to(w.device, torch.float32))
     return torch.matmul(h, w.view(k // 128, 128, n)).view(k, n)
 
 
 def had_right(w: torch.Tensor, h: torch.Tensor) -> torch.Tensor:
     """Block-128 Hadamard applied on the last (n) dim of w [k, n]
-    (quantize.py:141-145); on the GPU the left transform of the transpose
-    (h is symmetric: the same products in the same order)."""
+    (quantize.py:141-145); on the GPU the left transform of the transpose,
+    w @ h = (h^T @ w^T)^T (for the symmetric Hadamard the same products in
+    the same order as the CPU matmul)."""
     k, n = w.shape
     assert n % 128 == 0
     if w.is_cuda and w.dtype == torch.float32:
-        return had_left(w.t().contiguous(), h).t().contiguous()
+        return had_left(w.t().contiguous(), h.t()).t().contiguous()
     return torch.matmul(w.view(k, n // 128, 128), h).view(k, n)
 
 
@@ -383,6 +384,13 @@ def _launch(X: torch.Tensor, K: int, code: str, pivot: int, margin: int):
                         sync=False)
 
 
+def _lazy_cols(buf_cols) -> int:
+    """Columns of the lazy feedback buffer: whole 16-column blocks, at least
+    one, as the reference's buf_tiles = max(1, buf_cols // 16)
+    (quantize.py:665) -- so buf_cols = 8 or 100 run as 16 and 96."""
+    return 16 * max(1, int(buf_cols) // 16)
+
+
 def ldlq_viterbi(Wq: torch.Tensor, Lfac: torch.Tensor | None, lut: torch.Tensor,
                  K: int, L: int, buf_cols: int = 128, V: int = 1,
                  batch: int = 0, dtype: torch.dtype = torch.float32,
@@ -429,7 +437,7 @@ def ldlq_viterbi(Wq: torch.Tensor, Lfac: torch.Tensor | None, lut: torch.Tensor,
         Lg = Lfac.to(gdev, torch.float32).contiguous() if feedback else None
         hatW, states, trellis, xt = _hb.ldlq_chain(
             Wg, Lg, K, piv, int(margin), code=kcode, states=True,
-            targets=bool(ldlq_viterbi.keep_targets), buf_cols=int(buf_cols))
+            targets=bool(ldlq_viterbi.keep_targets), buf_cols=_lazy_cols(buf_cols))
         _chain_progress(progress, tk)
         ldlq_viterbi.last_trellis = trellis
         ldlq_viterbi.last_targets = xt
@@ -441,7 +449,7 @@ def ldlq_viterbi(Wq: torch.Tensor, Lfac: torch.Tensor | None, lut: torch.Tensor,
     prod = torch.zeros(k, n, dtype=Wq.dtype, device=dev)
     states = torch.empty(tk, tn, 256, dtype=torch.int32, device=gdev)
     trellis = torch.empty(tk, tn, 16 * K, dtype=torch.int16, device=gdev)
-    per_buf = max(1, buf_cols // 16)
+    per_buf = _lazy_cols(buf_cols) // 16
     step_i = 0
     for cur in range(tk, 0, -per_buf):
         lo = max(0, cur - per_buf)
@@ -664,7 +672,7 @@ def quantize_linear_group(Ws, H_x: torch.Tensor | None, code: str = "exl3_mul1",
             Lfac.to(gdev, torch.float32).contiguous() if feedback else None, None, 128,
             int(margin), code=_hb.code_name(_kernel_code(lut, L)), states=True,
             targets=bool(ldlq_viterbi.keep_targets), groups=[(r[1], r[2]) for r in runs],
-            buf_cols=int(buf_cols))
+            buf_cols=_lazy_cols(buf_cols))
         states = st.long().to(dev)
         hatWq = hatWq.to(dev)
         ldlq_viterbi.last_targets = xt
@@ -740,16 +748,25 @@ def quantize(W_transformed: torch.Tensor, U_upper: torch.Tensor | None,
              dtype: torch.dtype = torch.float32,
              backend: str = "hip", margin: int = 16, batch: int = 0,
              su_mag: torch.Tensor | None = None,
-             sv_mag: torch.Tensor | None = None):
+             sv_mag: torch.Tensor | None = None,
+             reference_arithmetic: bool = False):
     """Harness entry point (quantize.py:894-966).
 
     W_transformed [out, in] fp32 already in the inner (incoherent) domain;
     U_upper [in, in] the GPTQ-convention factor with U^T U = G^-1 (or None
     for plain tail-biting Viterbi); seed picks the pass-1 pivot (seed mod 256).
     su_mag/sv_mag fold per-channel magnitudes out before quantization and back
-    into W_hat.  Runs on W_transformed's device.  Returns (W_hat [out, in] fp32,
-    packed int16 [in/16, out/16, 16K], scale) with decode(packed) * scale ==
-    W_hat bit for bit (before the magnitude refold).
+    into W_hat.  Runs on W_transformed's device; the U -> L conversion runs on
+    U_upper's.  Returns (W_hat [out, in] fp32, packed int16 [in/16, out/16,
+    16K], scale) with decode(packed) * scale == W_hat bit for bit (before the
+    magnitude refold).
+
+    On the GPU the sweep's feedback already rounds as the reference's CPU
+    arithmetic does; the scale (a mean over the weight) and, for a device
+    U_upper, the U -> L conversion round differently there.
+    reference_arithmetic=True runs both on the host CPU, as torch computes
+    them for the reference, so that every output equals the reference's
+    CPU result bit for bit.
     """
     m_out, k_in = W_transformed.shape
     assert k_in % 16 == 0 and m_out % 16 == 0, W_transformed.shape
@@ -764,11 +781,12 @@ def quantize(W_transformed: torch.Tensor, U_upper: torch.Tensor | None,
                 else sv_mag.float().to(Wt.device))
         Wt = Wt / (sv_m.unsqueeze(1) * su_m.unsqueeze(0))
     Wq = Wt.t().contiguous()
-    scale = Wq.square().mean().sqrt() / lut_rms
+    host = bool(reference_arithmetic) and Wq.device.type != "cpu"
+    scale = ((_to_host(Wq) if host else Wq).square().mean().sqrt() / lut_rms).to(Wq.device)
     Wq = Wq / scale
     Lfac = None
     if U_upper is not None:
-        Uu = U_upper.double()
+        Uu = (_to_host(U_upper) if reference_arithmetic else U_upper).double()
         eye = torch.eye(Uu.shape[0], dtype=Uu.dtype, device=Uu.device)
         Ui = torch.linalg.solve_triangular(Uu, eye, upper=True)     # U^-1
         Lfac, _ = block_LDL(Ui @ Ui.t(), 16)                         # G = U^-1 U^-T

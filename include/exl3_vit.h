@@ -36,6 +36,8 @@
  *      pivot, its torch path asserts)
  *  11  a target is NaN
  *  12  null or misaligned pointer argument
+ *  13  a synchronous entry was given a stream that is being captured into a
+ *      HIP graph (nothing was enqueued; the capture is left intact)
  *
  * Environment (read on every call):
  *   XTQ_VIT_DEVIDX   device index for the host-pointer entries (default: the
@@ -48,8 +50,8 @@
  *                    64 GiB; no reference counterpart)
  *   XTQ_VIT_SCRATCH  backpointer scratch budget in bytes; larger batches are
  *                    processed in chunks (default 8 GiB)
- *   XTQ_VIT_DEFER    0: never, 1: always (K >= 4) run the deferred-argmin
- *                    encode; default: K >= 4 and batches of >= 8192 sequences
+ *   XTQ_VIT_DEFER    1: run the deferred-argmin encode for K >= 4 (opt-in);
+ *                    unset or any other value: never
  *   XTQ_VIT_DEFER_SCRATCH  scratch budget of the deferred-argmin encode's
  *                    minima rows (default 48 GiB, at most half of the free
  *                    device memory)
@@ -137,8 +139,11 @@ XTQ_API int xtq_vit_tailbite_dev_async(const float* dX, int nseq, int K, const c
 
 /*
  * xtq_vit_tailbite_dev without any device allocation.  No reference
- * counterpart: for callers that cannot allocate device memory (code under
- * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * counterpart: for callers that cannot allocate device memory (tight serving
+ * loops, harnesses that forbid hipMalloc).  It is synchronous -- it ends by
+ * reading its status word back and waiting for `stream` -- so it cannot be
+ * recorded into a HIP graph: on a stream under capture it returns 13 before
+ * enqueuing anything, and the capture stays valid.
  * The caller passes inputs and outputs as for xtq_vit_tailbite_dev; the
  * backpointers and per-sequence words live in a fixed 256 MiB array in the
  * library's code object (one copy per device, held until the process ends),
@@ -245,16 +250,19 @@ XTQ_API int xtq_trellis_unpack_dev(const int16_t* d_trellis, int nt, int K, int3
                            void* stream);
 
 /*
- * Device-pointer block-128 Hadamard on the first dimension: the HIP
- * counterpart of had_left (quantize.py:134-138), d_out = blockdiag(d_h) @ d_in
- * for [rows][cols] fp32 row-major buffers (rows a multiple of 128, d_out not
- * d_in), d_h the [128][128] normalised Sylvester matrix of hadamard128
- * (quantize.py:123-131).  Each output is one fp32 fused multiply-add chain
- * over the 128 products in ascending order, as torch's CPU sgemm evaluates
- * the reference's matmul, so results equal the reference's CPU results bit
- * for bit.  had_right is this entry on the transpose.  Stream-ordered.
+ * Device-pointer block-128 transform on the first dimension: the HIP
+ * counterpart of had_left (quantize.py:134-138).  d_ht holds the [128][128]
+ * multipliers by input row, d_ht[t][r] the weight of input row t in output
+ * row r, so d_out = blockdiag(d_ht^T) @ d_in for [rows][cols] fp32 row-major
+ * buffers (rows a multiple of 128, d_out not d_in).  For had_left(w, h) pass
+ * h^T; the normalised Sylvester matrix of hadamard128 (quantize.py:123-131)
+ * is symmetric, so it is passed as it is.  Each output is one fp32 fused
+ * multiply-add chain over the 128 products in ascending order, as torch's
+ * CPU sgemm evaluates the reference's matmul, so results equal the
+ * reference's CPU results bit for bit.  had_right is this entry on the
+ * transpose.  Stream-ordered.
  */
-XTQ_API int xtq_had128_left_dev(const float* d_h, const float* d_in, float* d_out, int rows,
+XTQ_API int xtq_had128_left_dev(const float* d_ht, const float* d_in, float* d_out, int rows,
                                 int cols, void* stream);
 
 /*
@@ -271,9 +279,9 @@ XTQ_API int64_t xtq_vit_scratch_per_seq(int K);
  * chunk a tail-bite of nseq sequences at K would run in on the current
  * device with the current environment, and in *deferred (nullable) 1 when
  * it would take the deferred-argmin encode (group minima rows in HBM, the
- * argmin recomputed by the traceback; K >= 4 and nseq >= 8192 by default,
- * XTQ_VIT_DEFER=0/1 to force), else 0.  Returns minus a status code on
- * error.  Sets the device up like any other entry point.
+ * argmin recomputed by the traceback; only with XTQ_VIT_DEFER=1 and
+ * K >= 4), else 0.  Returns minus a status code on error.  Sets the device
+ * up like any other entry point.
  */
 XTQ_API int xtq_vit_chunk_seqs(int nseq, int K, int* deferred);
 

@@ -98,6 +98,7 @@ def test_status_codes_without_device(lib):
     assert chm(fake, None, 64, 64, 2, i2(32, 32), i2(4, 7), *args, tp1, None, None) == 12
     assert chm(fake, None, 64, 64, 2, None, i2(4, 7), *args, tp2, None, None) == 12
     assert lib.xtq_vit_strerror(11) == b"NaN target"
+    assert lib.xtq_vit_strerror(13) == b"synchronous entry given a stream under graph capture"
     assert lib.xtq_vit_strerror(99) == b"unknown status"
 
 

@@ -220,8 +220,9 @@ def test_chain_vs_block_schedule(xq, monkeypatch):
     """quantize_linear on GPU tensors with the sweep as column chains and as
     the reference's block schedule, whose feedback then runs as torch GPU
     GEMMs (rounding unlike the reference's CPU order, which the chain
-    follows): the same encoder on targets that differ by an ulp here and
-    there, so the proxy losses agree closely."""
+    follows): the same encoder on targets that may differ by an ulp here and
+    there.  Measured: every tile identical, the proxy losses equal; held to
+    at most 1 % of tiles differing and a relative proxy change of 1e-5."""
     import workloads as wl
     g = torch.Generator().manual_seed(11)
     W = 0.02 * torch.randn(256, 512, generator=g)
@@ -235,7 +236,8 @@ def test_chain_vs_block_schedule(xq, monkeypatch):
     e_c, e_b = res["chain"][1], res["block"][1]
     same = (res["chain"][0]["trellis"] == res["block"][0]["trellis"]).all(dim=-1).float().mean()
     print(f"proxy chain {e_c:.6e} block {e_b:.6e}, identical tiles {float(same):.3f}")
-    assert abs(e_c - e_b) <= 0.01 * e_b
+    assert float(same) >= 0.99
+    assert abs(e_c - e_b) <= 1e-5 * e_b
 
 
 @pytest.mark.parametrize("cs,ldlq", [(False, True), (True, True), (True, False)])
@@ -451,6 +453,29 @@ def test_chain_equals_cpu_block_schedule(xq, hb, cpu8, K, shape):
     bad = int((sc.cpu() != sb).any(dim=-1).sum())
     assert bad == 0, f"{bad} of {sb.shape[0] * sb.shape[1]} tiles differ"
     assert torch.equal(hc.cpu(), hb_)
+
+
+@pytest.mark.parametrize("given,runs_as", [(100, 96), (8, 16), (17, 16)])
+def test_buffer_width_rounds_like_reference(xq, given, runs_as):
+    """A lazy-buffer width that is not a whole number of 16-column blocks runs
+    as the reference's buf_tiles = max(1, buf_cols // 16) blocks
+    (quantize.py:665): on the GPU chain and the CPU block schedule alike."""
+    import workloads as wl
+    k, n = 384, 64
+    g = torch.Generator().manual_seed(given)
+    Wq = torch.randn(k, n, generator=g)
+    G = wl.ar1_gram(k, 2 * k, 0.5, given)
+    G.diagonal().add_(0.01 * G.diagonal().mean())
+    Lf, _ = xq.block_LDL(G, 16)
+    lut = xq.get_lut("exl3_mul1")
+    print(f"case buf_cols {given} as {runs_as}", flush=True)
+    hw, sw = xq.ldlq_viterbi(Wq.cuda(), Lf.cuda(), lut.cuda(), 4, 16, margin=0,
+                             buf_cols=runs_as, schedule="chain")
+    hg, sg = xq.ldlq_viterbi(Wq.cuda(), Lf.cuda(), lut.cuda(), 4, 16, margin=0,
+                             buf_cols=given, schedule="chain")
+    assert torch.equal(sg, sw) and torch.equal(hg, hw)
+    hb_, sb = xq.ldlq_viterbi(Wq, Lf, lut, 4, 16, margin=0, buf_cols=given, schedule="block")
+    assert torch.equal(sb, sw.cpu()) and torch.equal(hb_, hw.cpu())
 
 
 def test_chain_factor_over_2g_elements(hb, oracle_mod, mul1_lut):

@@ -74,13 +74,14 @@ def _every_tile(hb, trellis: torch.Tensor, K: int) -> torch.Tensor:
     return st
 
 
-def _oracle_rows(O, lut, xt: torch.Tensor, st: torch.Tensor, rows, K: int, label: str):
+def _oracle_rows(O, lut, xt: torch.Tensor, st: torch.Tensor, rows, K: int, label: str,
+                 pivot: int = 128, margin: int = 0):
     """States of block rows `rows` against the C oracle on the kernel's own
     targets xt [tk, tn, 256]; st [tk, tn, 256]."""
     checked = 0
     for i in rows:
         X = xt[i].cpu().numpy()
-        want = O.tailbite(X, lut, K, 16, pivot=128, margin=0, nthreads=NTHREADS)
+        want = O.tailbite(X, lut, K, 16, pivot=pivot, margin=margin, nthreads=NTHREADS)
         got = st[i].cpu().numpy()
         bad = np.nonzero((got != want).any(axis=1))[0]
         assert bad.size == 0, f"{label}: block row {i}: tiles {bad[:8].tolist()} differ"
@@ -225,6 +226,60 @@ def test_c5_full_size(xq, hb, c5, oracle_mod, K):
     print(f"case c5 5120x17408 K={K}", flush=True)
     _run_config(xq, hb, oracle_mod, [c5["W"]], c5["H"], K, False, 8, f"c5 K={K}",
                 every_tile=(K == 4))
+
+
+def test_c5_harness_quantize(xq, hb, c5, oracle_mod):
+    """The reference's whole-tensor verification path at c5's shape
+    (check_tensor_bitexact.py:45-66,93-123): the weight taken to the inner
+    domain and the harness-convention factor U (U^T U = G^-1 of the rotated,
+    1 %-damped Hessian, built in fp64), then quantize() with seed 20261011
+    (pivot 147) and margin 16 at K=4 -- the U -> L conversion, the sweep and
+    the checks all on the GPU.  Every tile: wrap invariant, pack/unpack round
+    trip, decode x scale == W_hat, and its states against the reference's
+    torch Viterbi run on the GPU on the kernel's own targets; 8 block rows
+    spread over the sweep against the C oracle."""
+    seed, pivot, margin, K = 20261011, 147, 16, 4
+    assert seed % 256 == pivot
+    print(f"case c5 quantize() harness: U factor, seed {seed}, margin {margin}, K={K}",
+          flush=True)
+    dev = torch.device("cuda")
+    W = c5["W"].float().to(dev)                          # [5120 out, 17408 in]
+    k_in, m_out = W.shape[1], W.shape[0]
+    suh = xq.sign_vec(k_in, seed, dev).half()
+    svh = xq.sign_vec(m_out, seed + 1, dev).half()
+    h = xq.hadamard128(dev, torch.float32)
+    W_t = xq.to_inner(W.t().contiguous(), suh, svh, h).t().contiguous()   # [out, in]
+    del W
+    G = xq.rotate_hessian(c5["H"].float().to(dev), suh, h)
+    G.diagonal().add_(0.01 * G.diagonal().mean())
+    Gi = torch.cholesky_inverse(torch.linalg.cholesky(G.double()))
+    del G
+    U = torch.linalg.cholesky(Gi, upper=True)
+    err = float((U.t() @ U - Gi).abs().max())
+    del Gi
+    U = U.float()
+    print(f"U built on the GPU, |U^T U - G^-1| max {err:.2e}", flush=True)
+    xq.ldlq_viterbi.keep_targets = True
+    try:
+        W_hat, packed, scale = xq.quantize(W_t, U, "exl3_mul1", K, seed, margin=margin)
+        xt = xq.ldlq_viterbi.last_targets
+    finally:
+        xq.ldlq_viterbi.keep_targets = False
+        xq.ldlq_viterbi.last_targets = None
+    del U
+    tk, tn = k_in // 16, m_out // 16
+    assert packed.shape == (tk, tn, 16 * K) and W_hat.shape == (m_out, k_in)
+    st = _every_tile(hb, packed, K).view(tk, tn, 256)
+    assert torch.equal((hb.decode(packed.to(dev), K) * scale).t().contiguous(), W_hat), \
+        "decode(packed) x scale does not reproduce W_hat"
+    lut = oracle_mod.code_lut("exl3_mul1")
+    _oracle_rows(oracle_mod, lut, xt, st, _sample_rows(tk, 8), K, "c5 harness",
+                 pivot=pivot, margin=margin)
+    _every_tile_vs_port(torch.from_numpy(lut).to(dev), xt.reshape(-1, 256),
+                        st.reshape(-1, 256), K, "c5 harness", pivot=pivot, margin=margin)
+    rel = xq.rel_mse(W_t, W_hat)
+    print(f"c5 harness: rel MSE {rel:.4e}, scale {scale:.6e}", flush=True)
+    assert 0.0 < rel < 0.02
 
 
 def test_headline_batch_every_chunk(hb, wl, oracle_mod):

@@ -114,13 +114,20 @@ def test_quantize_linear_mid_golden(xq, cpu8, tag, K, cs):
         assert rel <= 1e-4
 
 
+# Measured on the MI355X for the default GPU pipeline against the
+# reference's CPU run: differing tile share and proxy-loss change, bounded at
+# twice the measurement (k4: no tile differs; the bound allows 4 of 4,096).
+MID_GPU_BOUNDS = {"k4": (4 / 4096, 2e-7), "k5cs": (0.0156, 3.1e-5)}
+
+
 @pytest.mark.parametrize("tag,K,cs", [("k4", 4, False), ("k5cs", 5, True)])
 def test_quantize_linear_mid_on_gpu_vs_reference(xq, tag, K, cs):
     """The same weight with every step on the GPU (column-chain schedule):
-    the GPU's rotations, factorisation and feedback round differently from
-    the reference's CPU arithmetic, so a few tiles' targets move by an ulp and
-    encode differently; the differing share and the proxy-loss change are
-    reported and bounded."""
+    the GPU's reductions and factorisation round differently from the
+    reference's CPU arithmetic (the chain's feedback follows the reference's
+    order), so a few tiles' targets move by an ulp and encode differently;
+    the differing share and the proxy-loss change are held to twice what
+    they measure (0 % / 7.6e-8 for k4, 0.78 % / 1.5e-5 for k5cs)."""
     e = load_golden("e2e_mid.npz")
     W = torch.from_numpy(e["W16"].astype(np.float32))
     H = _kms_hessian(1024)
@@ -132,7 +139,8 @@ def test_quantize_linear_mid_on_gpu_vs_reference(xq, tag, K, cs):
     rel = abs(herr - float(e[f"{tag}_herr64"])) / abs(float(e[f"{tag}_herr64"]))
     print(f"{tag}: {100 * differ:.2f} % of tiles differ from the reference's CPU run, "
           f"proxy loss {herr:.6e} vs {float(e[f'{tag}_herr']):.6e} (rel {rel:.2e})", flush=True)
-    assert differ <= 0.05 and rel <= 1e-3
+    max_differ, max_rel = MID_GPU_BOUNDS[tag]
+    assert differ <= max_differ and rel <= max_rel
 
 
 @pytest.mark.parametrize("tag,K,cs", [("k4", 4, False), ("k5cs", 5, True)])
@@ -227,6 +235,16 @@ def test_hadamard_kernel_matches_cpu(xq, k, n):
         Hx = w @ w.t() / n
         assert torch.equal(xq.rotate_hessian(Hx.cuda(), xq.sign_vec(k, 5).cuda(), hd).cpu(),
                            xq.rotate_hessian(Hx, xq.sign_vec(k, 5), h))
+    # any 128x128 matrix, not only the symmetric Hadamard: h @ w and w @ h
+    hn = torch.randn(128, 128, generator=g)
+    assert not torch.equal(hn, hn.t())
+    want = xq.had_left(w.double(), hn.double()).float()
+    got = xq.had_left(w.cuda(), hn.cuda()).cpu()
+    torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
+    if n % 128 == 0:
+        want = xq.had_right(w.double(), hn.double()).float()
+        got = xq.had_right(w.cuda(), hn.cuda()).cpu()
+        torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
 
 
 def test_quantize_harness_golden(xq, cpu8):
@@ -395,9 +413,11 @@ def test_quantize_with_U_on_device(xq, oracle_mod, mul1_lut, cpu8):
     U -> L conversion (triangular solve, G = U^-1 U^-T, block LDL) runs on
     the GPU in fp64 and agrees with the CPU conversion to fp64 rounding; the
     sweep (column chains) encodes every tile bit-exactly for the targets the
-    kernel computed; the result matches the reference's golden output up to
-    the feedback rounding of the GPU (its fp32 sums are not the CPU GEMM's,
-    so a tile whose targets move by an ulp may encode differently)."""
+    kernel computed.  Against the reference's golden output: the sweep's
+    feedback follows the reference's order, but the scale is a device mean
+    and the factor the GPU's, so a tile whose targets move by an ulp may
+    encode differently; with reference_arithmetic=True (scale and U -> L on
+    the host) every output equals the golden one bit for bit."""
     e = load_golden("e2e_128.npz")
     Wt = torch.from_numpy(e["prep_Wt"])
     U = torch.from_numpy(e["q_U"])
@@ -433,6 +453,14 @@ def test_quantize_with_U_on_device(xq, oracle_mod, mul1_lut, cpu8):
           flush=True)
     assert diff_tiles <= 4
     assert abs(e_gpu - e_ref) <= 1e-2 * e_ref
+    print("case quantize() with U on cuda, reference_arithmetic", flush=True)
+    for Ud in (U.cuda(), U):                  # device or host factor
+        W_hat, packed, scale = xq.quantize(Wt.cuda(), Ud, "exl3_mul1", 4, seed=147, margin=16,
+                                           reference_arithmetic=True)
+        assert W_hat.is_cuda and packed.is_cuda
+        np.testing.assert_array_equal(packed.cpu().numpy(), e["q_packed"])
+        np.testing.assert_array_equal(W_hat.cpu().numpy(), e["q_W_hat"])
+        assert np.float32(scale) == e["q_scale"]
 
 
 def test_factor_hessian_fallback_on_device(xq):

@@ -241,6 +241,20 @@ def test_deferred_chunks(hb, oracle_mod, mul1_lut, K, monkeypatch):
     np.testing.assert_array_equal(got[idx].cpu().numpy(), want)
 
 
+def test_defer_is_opt_in(hb, monkeypatch):
+    """The deferred-argmin encode runs only with XTQ_VIT_DEFER=1 and K >= 4:
+    unset, "0" or any other value leave every batch on the key-argmin
+    forward (xtq_vit_chunk_seqs reports the path a batch would take)."""
+    monkeypatch.delenv("XTQ_VIT_DEFER", raising=False)
+    for K in (2, 4, 7):
+        for n in (64, 8192, 348160):
+            assert hb.chunk_seqs(n, K)[1] == 0
+    for v, want in (("0", 0), ("yes", 0), ("1", 1)):
+        monkeypatch.setenv("XTQ_VIT_DEFER", v)
+        assert hb.chunk_seqs(8192, 4)[1] == want
+        assert hb.chunk_seqs(8192, 3)[1] == 0
+
+
 @pytest.mark.parametrize("K", (2, 4, 7))
 def test_forced_chunks(hb, oracle_mod, mul1_lut, K, monkeypatch):
     """XTQ_VIT_SCRATCH is read on every call: a budget of 2048 sequences
