@@ -217,6 +217,10 @@ __device__ __forceinline__ int bp_lookup(const uint8_t* row, int j) {
 template <int K, int T>
 constexpr bool kGroupOps = (K >= 6) || ((K == 4 || K == 5) && T >= 2);
 
+// The same choice for the min-only steps.
+template <int K, int T>
+constexpr bool kGroupOpsMin = kGroupOps<K, T>;
+
 // Candidates per chunk of the min tree: 8 wherever the smaller chunk's keys
 // make room for the fp32 codebook registers -- every K at T = 1 (the column
 // chain) and K != 6 at any T (16-wide chunks spilled there: K=5 batched
@@ -227,6 +231,11 @@ constexpr bool kGroupOps = (K >= 6) || ((K == 4 || K == 5) && T >= 2);
 template <int K, int T>
 constexpr int kChunkW =
     (T == 1 || K != 6) ? (Geom<K>::NCH < 8 ? Geom<K>::NCH : 8) : Geom<K>::NCH;
+
+// Candidates per chunk in the min-only steps (fp32 costs, no keys): the same
+// widths.
+template <int K, int T>
+constexpr int kChunkWMin = kChunkW<K, T>;
 
 // Wave priorities within a step (s_setprio).  All 16 waves meet at the
 // step's barrier, and the SIMD's arbiter otherwise serves its oldest wave
@@ -303,8 +312,7 @@ __device__ __forceinline__ void fwd_run(
     // group is state j_c + (wbase + w) * SP; local index l = c*W + w.
     const int jbase = G::HALF ? (tid >> 1) : tid * G::C;
     const int wbase = G::HALF ? (tid & 1) * G::W : 0;
-    constexpr int NCH = kChunkW<K, T>;          // candidates per chunk
-    constexpr int NCHUNK = G::W / NCH;
+    constexpr int NCHK = kChunkW<K, T>;         // candidates per chunk (key steps)
     // codebook value of local state l, exact in fp32
     float f32[G::NSTATE];
 #pragma unroll
@@ -316,9 +324,9 @@ __device__ __forceinline__ void fwd_run(
     auto fsub = [&](int l, float negx) { return f32[l] + negx; };
     // Per-lane key tags: distinct per lane so they stay in VGPRs next to the
     // cost they are paired with; the low byte is the candidate index.
-    uint32_t tag[NCH];
+    uint32_t tag[NCHK];
 #pragma unroll
-    for (int w = 0; w < NCH; ++w) tag[w] = ((uint32_t)tid << 8) | (uint32_t)(wbase + w);
+    for (int w = 0; w < NCHK; ++w) tag[w] = ((uint32_t)tid << 8) | (uint32_t)(wbase + w);
     __syncthreads();
 
     // Start mask b_0: 0 everywhere (free) or 0 only at group ov (pinned).
@@ -351,6 +359,8 @@ __device__ __forceinline__ void fwd_run(
     auto step = [&](auto keys_c, int i) __attribute__((always_inline)) {
         constexpr bool KEYS = decltype(keys_c)::value;
         typedef typename RunType<KEYS>::type run_t;
+        constexpr int NCH = KEYS ? kChunkW<K, T> : kChunkWMin<K, T>;  // candidates per chunk
+        constexpr int NCHUNK = G::W / NCH;
         // Target of step i of the sequence rolled right by `roll`.
         const int u = (i - roll < 0) ? i - roll + xlen : i - roll;
 #pragma unroll 1
@@ -412,7 +422,7 @@ __device__ __forceinline__ void fwd_run(
                     }
                     // candidate costs fl(fl(fl(f - x)^2) + b)
                     float dv[NCH];
-                    if constexpr (kGroupOps<K, T>) {
+                    if constexpr (KEYS ? kGroupOps<K, T> : kGroupOpsMin<K, T>) {
                         // Issue the chunk's candidates opcode by opcode (all
                         // subs, then all squares, then all adds): gfx950
                         // issues adjacent independent v_mul_f32 / v_add_f32
