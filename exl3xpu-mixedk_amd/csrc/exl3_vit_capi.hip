@@ -22,7 +22,7 @@
 
 namespace {
 
-enum Code { kMul1 = 0, k3Inst = 1, kMcg = 2, kNumCodes = 3 };
+enum Code { kMul1 = 0, k3Inst = 1, kMcg = 2, k1Mad = 3, kNumCodes = 4 };
 
 // --------------------------------------------------------- codebook tables
 // fp16 bits -> double (exact).
@@ -53,20 +53,28 @@ uint16_t double_to_half(double v) {
     return sgn | (uint16_t)(((ue + 15) << 10) | ((int)q - 1024));
 }
 
-// Codebook tables, restating quantize.py:56-81 (_local_code_lut).
-void make_lut16(Code code, uint16_t* out) {
+// Codebook tables as the fp32 values the reference's get_lut returns,
+// restating quantize.py:56-87 (_local_code_lut): the EXL3 codes round to
+// fp16 (held exactly in fp32); qtip_1mad divides in double and rounds once
+// to fp32, as numpy's astype(float32) does.
+void make_lut(Code code, float* out) {
     for (uint32_t s = 0; s < 65536u; ++s) {
         if (code == kMul1) {
             const uint32_t x = s * 0x83DCD12Du;
             const uint32_t bs = (x & 0xFF) + ((x >> 8) & 0xFF) + ((x >> 16) & 0xFF) + (x >> 24);
             const double h = 1024.0 + bs;
-            out[s] = double_to_half(h * half_to_double(0x1EEE) + half_to_double(0xC931));
+            out[s] = (float)half_to_double(
+                double_to_half(h * half_to_double(0x1EEE) + half_to_double(0xC931)));
+        } else if (code == k1Mad) {
+            const uint32_t x = s * 34038481u + 76625530u;
+            const uint32_t bs = (x & 0xFF) + ((x >> 8) & 0xFF) + ((x >> 16) & 0xFF) + (x >> 24);
+            out[s] = (float)(((double)bs - 510.0) / 147.800537109375);
         } else {
             uint32_t x = (code == k3Inst) ? s * 89226354u + 64248484u : s * 0xCBAC1FEDu;
             x = (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
             const double lo = half_to_double((uint16_t)(x & 0xFFFF));
             const double hi = half_to_double((uint16_t)(x >> 16));
-            out[s] = double_to_half(lo + hi);
+            out[s] = (float)half_to_double(double_to_half(lo + hi));
         }
     }
 }
@@ -76,6 +84,7 @@ int parse_code(const char* code, Code* out) {
     if (!strcmp(code, "mul1") || !strcmp(code, "exl3_mul1")) { *out = kMul1; return 0; }
     if (!strcmp(code, "3inst") || !strcmp(code, "exl3_3inst")) { *out = k3Inst; return 0; }
     if (!strcmp(code, "mcg") || !strcmp(code, "exl3_mcg")) { *out = kMcg; return 0; }
+    if (!strcmp(code, "1mad") || !strcmp(code, "qtip_1mad")) { *out = k1Mad; return 0; }
     return 8;
 }
 
@@ -86,7 +95,7 @@ constexpr int kMaxChainGroups = 8;
 struct DevCtx {
     bool ready = false;
     int ncu = 0;
-    uint16_t* lut16[kNumCodes] = {nullptr, nullptr, nullptr};
+    float* lut[kNumCodes] = {};               // fp32 codebook tables
     uint32_t* err = nullptr;
     void* bp = nullptr;
     size_t bp_cap = 0;
@@ -219,11 +228,11 @@ int dev_init(int dev) {
     if (cx.ready) return 0;
     if (hipDeviceGetAttribute(&cx.ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         return 1;
-    std::vector<uint16_t> h(65536);
+    std::vector<float> h(65536);
     for (int c = 0; c < kNumCodes; ++c) {
-        if (hipMalloc((void**)&cx.lut16[c], 65536 * sizeof(uint16_t)) != hipSuccess) return 2;
-        make_lut16((Code)c, h.data());
-        if (hipMemcpy(cx.lut16[c], h.data(), 65536 * sizeof(uint16_t), hipMemcpyHostToDevice) !=
+        if (hipMalloc((void**)&cx.lut[c], 65536 * sizeof(float)) != hipSuccess) return 2;
+        make_lut((Code)c, h.data());
+        if (hipMemcpy(cx.lut[c], h.data(), 65536 * sizeof(float), hipMemcpyHostToDevice) !=
             hipSuccess)
             return 1;
     }
@@ -239,7 +248,7 @@ int dev_init(int dev) {
         return 1;
     }
     cx.noalloc = (uint8_t*)na;
-    cx.owned = kNumCodes * 65536 * sizeof(uint16_t) + 256;
+    cx.owned = kNumCodes * 65536 * sizeof(float) + 256;
     cx.ready = true;
     return 0;
 }
@@ -478,7 +487,7 @@ int tailbite_chunks(DevCtx& cx, const TbScratch& w, int chunk, const float* dX, 
                     int K, Code code, int margin, int pivot, int32_t* d_states,
                     int16_t* d_trellis, hipStream_t s, bool prof, bool defer = false) {
     const int n1 = (margin > 0 && pivot + margin < xtq::kSteps) ? pivot + margin : xtq::kSteps;
-    const uint16_t* lut = cx.lut16[code];
+    const float* lut = cx.lut[code];
     auto pbeg = [&](int kind, double steps) { return prof ? prof_begin(s, kind, steps) : -1; };
     for (int c0 = 0; c0 < nseq; c0 += chunk) {
         const int n = (nseq - c0) < chunk ? (nseq - c0) : chunk;
@@ -779,7 +788,7 @@ int run_ldlq_chain(DevCtx& cx, const float* W, const float* L, int k, int n,
             break;
         }
         e = xtq::launch_ldlq_chain(
-            Kg[g], W, L ? cx.Lt : nullptr, k, n, grp[g].jc0, grp[g].tnl, cx.lut16[code], pivot,
+            Kg[g], W, L ? cx.Lt : nullptr, k, n, grp[g].jc0, grp[g].tnl, cx.lut[code], pivot,
             n1, (uint8_t*)cx.bp + bp_off[g], nwg[g], targets ? targets : cx.xbuf + x_off[g] * xtq::kSteps,
             targets ? 1 : 0, hatW, cx.E, states, grp[g].trellis, cx.cflags, cx.ccount + g,
             cx.epoch, kSpinLimit, cx.err, buf_cols, sg);
@@ -805,7 +814,7 @@ int run_viterbi(DevCtx& cx, const float* dX, int nseq, int T, int K, Code code,
     int rc = reserve_scratch(cx, K, chunk);
     if (!rc) rc = scratch_begin(cx, s);
     if (rc) return rc;
-    const uint16_t* lut = cx.lut16[code];
+    const float* lut = cx.lut[code];
     const int stop = back_from >= 0 ? back_from : 0;
     for (int c0 = 0; c0 < nseq; c0 += chunk) {
         const int n = (nseq - c0) < chunk ? (nseq - c0) : chunk;
@@ -1099,7 +1108,7 @@ int xtq_trellis_decode_dev(const int16_t* d_trellis, int tk, int tn, int K, cons
     if (current_device(&dev)) return 1;
     rc = dev_init(dev);
     if (rc) return rc;
-    hipError_t e = xtq::launch_decode(K, d_trellis, tk, tn, g_dev[dev].lut16[c], d_out_f32,
+    hipError_t e = xtq::launch_decode(K, d_trellis, tk, tn, g_dev[dev].lut[c], d_out_f32,
                                       d_out_f16, (hipStream_t)stream);
     if (e != hipSuccess) {
         fprintf(stderr, "xtq_vit decode: %s\n", hipGetErrorString(e));
@@ -1154,9 +1163,7 @@ int xtq_vit_get_lut(const char* code, float* out) {
     Code c;
     int rc = parse_code(code, &c);
     if (rc) return rc;
-    std::vector<uint16_t> h(65536);
-    make_lut16(c, h.data());
-    for (int s = 0; s < 65536; ++s) out[s] = (float)half_to_double(h[s]);
+    make_lut(c, out);
     return 0;
 }
 

@@ -30,7 +30,7 @@ int forward_group(int K, int nseq, int ncu);
 
 // Forward DP of one Viterbi run for nseq sequences.
 //   X, xstride, xlen  targets: row q holds xlen fp32 values at X + q*xstride
-//   lut16   [65536] fp16 bit patterns of the codebook (device)
+//   lut     [65536] fp32 codebook values f(state) (device)
 //   roll    step i reads target (i - roll) mod xlen (roll != 0 needs xlen 256)
 //   nsteps  steps of the run (<= xlen when roll == 0)
 //   store_lo first step whose backpointers are kept (steps store_lo..nsteps-2)
@@ -40,14 +40,14 @@ int forward_group(int K, int nseq, int ncu);
 //   send    [nseq] final state of the run (device, out)
 //   err     device word, OR-ed with 1 when a target is NaN
 hipError_t launch_forward(int K, const float* X, int xstride, int xlen, int nseq,
-                          const uint16_t* lut16, int roll, int nsteps, int store_lo,
+                          const float* lut, int roll, int nsteps, int store_lo,
                           const int32_t* ov_in, void* bp, int32_t* send, uint32_t* err,
                           int group, hipStream_t stream);
 
 // launch_forward for K=3 (same arguments); defined in the K=3 translation
 // unit (viterbi_kernels.hip built with XTQ_FWD_K3_TU).
 hipError_t launch_forward_k3(const float* X, int xstride, int xlen, int nseq,
-                             const uint16_t* lut16, int roll, int nsteps, int store_lo,
+                             const float* lut, int roll, int nsteps, int store_lo,
                              const int32_t* ov_in, void* bp, int32_t* send, uint32_t* err,
                              int group, hipStream_t stream);
 
@@ -57,7 +57,7 @@ hipError_t launch_forward_k3(const float* X, int xstride, int xlen, int nseq,
 // row of 2^(16-K) floats per step, defer_tile_bytes(K) per sequence.
 size_t defer_tile_bytes(int K);
 hipError_t launch_forward_defer(int K, const float* X, int xstride, int xlen, int nseq,
-                                const uint16_t* lut16, int roll, int nsteps, int store_lo,
+                                const float* lut, int roll, int nsteps, int store_lo,
                                 const int32_t* ov_in, void* bm, int32_t* send, uint32_t* err,
                                 int group, hipStream_t stream);
 
@@ -66,7 +66,7 @@ hipError_t launch_forward_defer(int K, const float* X, int xstride, int xlen, in
 // rows, the codebook and the targets (X, xstride, xlen, roll as the forward
 // read them; ov_in the run's pins or NULL).  Outputs as launch_traceback.
 hipError_t launch_traceback_defer(int K, const void* bm, const float* X, int xstride, int xlen,
-                                  int roll, const uint16_t* lut16, int nseq,
+                                  int roll, const float* lut, int nseq,
                                   const int32_t* send, const int32_t* ov_in, int nsteps,
                                   int stop, int shift, int32_t* sout, int32_t* states,
                                   int16_t* trellis, hipStream_t stream);
@@ -80,7 +80,7 @@ hipError_t launch_traceback_defer(int K, const void* bm, const float* X, int xst
 // values != epoch on entry (epoch increases per launch; zero-filled memory
 // and epoch >= 1 work); counter is one device word.  err |= 2 when a pass-2
 // wait expires after spin_limit polls, |= 4 on a task outside the launch.
-hipError_t launch_tailbite_fused(int K, const float* X, int nseq, const uint16_t* lut16,
+hipError_t launch_tailbite_fused(int K, const float* X, int nseq, const float* lut,
                                  int pivot, int n1, void* bp, int32_t* send, int32_t* ovbuf,
                                  uint32_t* flags, int32_t* counter, uint32_t epoch,
                                  int spin_limit, uint32_t* err, hipStream_t stream);
@@ -113,7 +113,7 @@ hipError_t launch_had_left(const float* ht, const float* in, float* out, int row
 // (a multiple of 16) is the reference sweep's lazy-feedback buffer width,
 // which fixes the order the feedback is summed in.
 hipError_t launch_ldlq_chain(int K, const float* W, const float* Lq, int k, int n, int jc0,
-                             int tnl, const uint16_t* lut16, int pivot, int n1, void* bp,
+                             int tnl, const float* lut, int pivot, int n1, void* bp,
                              int nwg, float* xbuf, int xdump, float* hatW, float* Eq,
                              int32_t* states, int16_t* trellis, uint32_t* flags,
                              int32_t* counter, uint32_t epoch, int spin_limit, uint32_t* err,
@@ -133,7 +133,7 @@ hipError_t launch_traceback(int K, const void* bp, int nseq, const int32_t* send
 
 // Trellis decode: int16 [tk][tn][16K] -> [16tk][16tn] (fp32 or fp16 bits).
 hipError_t launch_decode(int K, const int16_t* trellis, int tk, int tn,
-                         const uint16_t* lut16, float* out_f32,
+                         const float* lut, float* out_f32,
                          uint16_t* out_f16, hipStream_t stream);
 
 // Pack / unpack between int32 states [nt][256] and int16 trellis [nt][16K].

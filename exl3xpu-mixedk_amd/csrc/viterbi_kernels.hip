@@ -14,9 +14,10 @@
 //   * thread t owns the C = SP/1024 consecutive groups j = t*C .. t*C+C-1
 //     (K=7: half of group t/2) and the candidate states of each,
 //     s = j + w*SP, i.e. 64 states per thread for every K; their codebook
-//     values (every supported codebook is fp16-exact, hence exact in fp32)
-//     stay in 64 fp32 VGPRs for the whole kernel, shared by the T
-//     sequences, so that fl(f - x) is one v_add_f32 of -x, an instruction
+//     values (the fp32 table of the reference's get_lut: fp16 values for
+//     the EXL3 codes, (bytesum - 510) / 147.8 rounded to fp32 for
+//     qtip_1mad) stay in 64 fp32 VGPRs for the whole kernel, shared by the
+//     T sequences, so that fl(f - x) is one v_add_f32 of -x, an instruction
 //     gfx950 issues on its fast path (the packed fp16 pairs plus
 //     v_fma_mix_f32 of earlier versions took 32 VGPRs but a full 4 cycles);
 //   * the per-group minima b (SP floats per sequence) are the only state
@@ -287,7 +288,7 @@ struct FwdSmem {
 template <int K, int T>
 __device__ __forceinline__ void fwd_run(
     FwdSmem<K, T>& sm, const float* __restrict__ X, int xstride, int xlen, int q0, int ntile,
-    const uint16_t* __restrict__ lut16, int roll, int nsteps, int store_lo, bool pinned,
+    const float* __restrict__ lut, int roll, int nsteps, int store_lo, bool pinned,
     uint8_t* __restrict__ bp, int32_t* send, uint32_t* __restrict__ err, int tid) {
     using G = Geom<K>;
     auto& bbuf = sm.bbuf;
@@ -313,12 +314,11 @@ __device__ __forceinline__ void fwd_run(
     const int jbase = G::HALF ? (tid >> 1) : tid * G::C;
     const int wbase = G::HALF ? (tid & 1) * G::W : 0;
     constexpr int NCHK = kChunkW<K, T>;         // candidates per chunk (key steps)
-    // codebook value of local state l, exact in fp32
+    // codebook value of local state l (the fp32 table entry)
     float f32[G::NSTATE];
 #pragma unroll
     for (int l = 0; l < G::NSTATE; ++l)
-        f32[l] = (float)__builtin_bit_cast(
-            _Float16, lut16[jbase + l / G::W + (wbase + l % G::W) * G::SP]);
+        f32[l] = lut[jbase + l / G::W + (wbase + l % G::W) * G::SP];
     // fl(f_l - x): one rounding of the exact difference, as the reference's
     // fp32 subtraction
     auto fsub = [&](int l, float negx) { return f32[l] + negx; };
@@ -614,7 +614,7 @@ __device__ __forceinline__ void fwd_run(
 template <int K, int T>
 __global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
     const float* __restrict__ X, int xstride, int xlen, int nseq,
-    const uint16_t* __restrict__ lut16, int roll, int nsteps, int store_lo,
+    const float* __restrict__ lut, int roll, int nsteps, int store_lo,
     const int32_t* __restrict__ ov_in,
     uint8_t* __restrict__ bp, int32_t* __restrict__ send, uint32_t* __restrict__ err) {
     __shared__ FwdSmem<K, T> sm;
@@ -623,7 +623,7 @@ __global__ __launch_bounds__(kFwdThreads) void fwd_kernel(
     const bool pinned = (ov_in != nullptr);
     if (threadIdx.x < T)
         sm.ovs[threadIdx.x] = (pinned && (int)threadIdx.x < ntile) ? ov_in[q0 + threadIdx.x] : -1;
-    fwd_run<K, T>(sm, X, xstride, xlen, q0, ntile, lut16, roll, nsteps, store_lo, pinned, bp,
+    fwd_run<K, T>(sm, X, xstride, xlen, q0, ntile, lut, roll, nsteps, store_lo, pinned, bp,
                   send + q0, err, (int)threadIdx.x);
 }
 
@@ -893,7 +893,7 @@ constexpr size_t defer_tile_bytes() {
 template <int K, int T>
 __device__ __forceinline__ void fwd_run_defer(
     FwdSmem<K, T>& sm, const float* __restrict__ X, int xstride, int xlen, int q0, int ntile,
-    const uint16_t* __restrict__ lut16, int roll, int nsteps, int store_lo, bool pinned,
+    const float* __restrict__ lut, int roll, int nsteps, int store_lo, bool pinned,
     float* __restrict__ bm, int32_t* send, uint32_t* __restrict__ err, int tid) {
     using G = Geom<K>;
     static_assert(K >= 4, "K = 2, 3 keep the key-argmin forward");
@@ -923,8 +923,7 @@ __device__ __forceinline__ void fwd_run_defer(
     float f32[G::NSTATE];
 #pragma unroll
     for (int l = 0; l < G::NSTATE; ++l)
-        f32[l] = (float)__builtin_bit_cast(
-            _Float16, lut16[jbase + l / G::W + (wbase + l % G::W) * G::SP]);
+        f32[l] = lut[jbase + l / G::W + (wbase + l % G::W) * G::SP];
     auto fsub = [&](int l, float negx) { return f32[l] + negx; };
     __syncthreads();
 
@@ -1054,7 +1053,7 @@ __device__ __forceinline__ void fwd_run_defer(
 #pragma unroll 8
         for (int k = 0; k < 65536 / kFwdThreads; ++k) {
             const int st_ = tid + k * kFwdThreads;
-            const float f = (float)__builtin_bit_cast(_Float16, lut16[st_]);
+            const float f = lut[st_];
             const float d = f + negx;
             const float cost = d * d + bcur[bslot<K>(st_ >> K)];
             const bool allowed = !pinned || ((st_ & (G::SP - 1)) == ov);
@@ -1079,7 +1078,7 @@ __device__ __forceinline__ void fwd_run_defer(
 template <int K, int T>
 __global__ __launch_bounds__(kFwdThreads) void fwd_defer_kernel(
     const float* __restrict__ X, int xstride, int xlen, int nseq,
-    const uint16_t* __restrict__ lut16, int roll, int nsteps, int store_lo,
+    const float* __restrict__ lut, int roll, int nsteps, int store_lo,
     const int32_t* __restrict__ ov_in, float* __restrict__ bm, int32_t* __restrict__ send,
     uint32_t* __restrict__ err) {
     __shared__ FwdSmem<K, T> sm;
@@ -1088,7 +1087,7 @@ __global__ __launch_bounds__(kFwdThreads) void fwd_defer_kernel(
     const bool pinned = (ov_in != nullptr);
     if (threadIdx.x < T)
         sm.ovs[threadIdx.x] = (pinned && (int)threadIdx.x < ntile) ? ov_in[q0 + threadIdx.x] : -1;
-    fwd_run_defer<K, T>(sm, X, xstride, xlen, q0, ntile, lut16, roll, nsteps, store_lo, pinned,
+    fwd_run_defer<K, T>(sm, X, xstride, xlen, q0, ntile, lut, roll, nsteps, store_lo, pinned,
                         bm, send + q0, err, (int)threadIdx.x);
 }
 
@@ -1105,7 +1104,7 @@ constexpr int kTbDeferChunk = 16;     // candidates recomputed per batch of load
 template <int K>
 __global__ __launch_bounds__(kTbLaneSeqs) void tb_defer_kernel(
     const float* __restrict__ bm, const float* __restrict__ X, int xstride, int xlen, int roll,
-    const uint16_t* __restrict__ lut16, int nseq, const int32_t* __restrict__ send,
+    const float* __restrict__ lut, int nseq, const int32_t* __restrict__ send,
     const int32_t* __restrict__ ov_in, int nsteps, int stop, int shift,
     int32_t* __restrict__ sout, int32_t* __restrict__ states, int16_t* __restrict__ trellis) {
     using G = Geom<K>;
@@ -1138,7 +1137,7 @@ __global__ __launch_bounds__(kTbLaneSeqs) void tb_defer_kernel(
                     const int g = a + (w0 + w) * G::Q;
                     bv[w] = (i - 1 == 0) ? ((ov < 0 || g == ov) ? 0.0f : __builtin_inff())
                                          : brow[(w0 + w) * G::Q];
-                    f[w] = (float)__builtin_bit_cast(_Float16, lut16[j + (w0 + w) * G::SP]);
+                    f[w] = lut[j + (w0 + w) * G::SP];
                 }
 #pragma unroll
                 for (int w = 0; w < CH; ++w) {
@@ -1188,7 +1187,7 @@ __global__ __launch_bounds__(kTbLaneSeqs) void tb_defer_kernel(
 // pass-2 traceback runs as tb_kernel afterwards.
 template <int K>
 __global__ __launch_bounds__(kFwdThreads) void tailbite_fused_kernel(
-    const float* __restrict__ X, int nseq, const uint16_t* __restrict__ lut16, int pivot,
+    const float* __restrict__ X, int nseq, const float* __restrict__ lut, int pivot,
     int n1, uint8_t* __restrict__ bp, int32_t* __restrict__ send, int32_t* __restrict__ ovbuf,
     uint32_t* __restrict__ flags, int32_t* __restrict__ counter, uint32_t epoch,
     int spin_limit, uint32_t* __restrict__ err) {
@@ -1205,7 +1204,7 @@ __global__ __launch_bounds__(kFwdThreads) void tailbite_fused_kernel(
     }
     if (t < nseq) {
         if (tid == 0) sm.ovs[0] = -1;
-        fwd_run<K, 1>(sm, X, kSteps, kSteps, t, 1, lut16, pivot, n1, pivot, false, bp, &cur,
+        fwd_run<K, 1>(sm, X, kSteps, kSteps, t, 1, lut, pivot, n1, pivot, false, bp, &cur,
                       err, tid);
         // This workgroup's backpointer stores reach L2 (and are written back
         // past it, since pass 2 of this sequence may run on another XCD and
@@ -1239,7 +1238,7 @@ __global__ __launch_bounds__(kFwdThreads) void tailbite_fused_kernel(
         }
         __syncthreads();
         if (sm.ovs[0] < 0) return;             // wait expired: reported through err
-        fwd_run<K, 1>(sm, X, kSteps, kSteps, q, 1, lut16, 0, kSteps, 0, true, bp, send + q,
+        fwd_run<K, 1>(sm, X, kSteps, kSteps, q, 1, lut, 0, kSteps, 0, true, bp, send + q,
                       err, tid);
     }
 }
@@ -1283,7 +1282,7 @@ __device__ __forceinline__ uint32_t window_state(const uint32_t* words, int t) {
 
 template <int K>
 __global__ __launch_bounds__(256) void decode_kernel(
-    const int16_t* __restrict__ trellis, int tn, const uint16_t* __restrict__ lut16,
+    const int16_t* __restrict__ trellis, int tn, const float* __restrict__ lut,
     float* __restrict__ out_f32, uint16_t* __restrict__ out_f16) {
     __shared__ uint32_t words[8 * K];
     const int tile = blockIdx.x, t = threadIdx.x;
@@ -1295,9 +1294,9 @@ __global__ __launch_bounds__(256) void decode_kernel(
     const int a = tile / tn, b = tile - a * tn;
     const size_t n = (size_t)tn * 16;
     const size_t idx = (size_t)(16 * a + (p >> 4)) * n + 16 * b + (p & 15);
-    const uint16_t h = lut16[s];
-    if (out_f32) out_f32[idx] = (float)__builtin_bit_cast(_Float16, h);
-    if (out_f16) out_f16[idx] = h;
+    const float v = lut[s];
+    if (out_f32) out_f32[idx] = v;
+    if (out_f16) out_f16[idx] = __builtin_bit_cast(uint16_t, (_Float16)v);
 }
 
 template <int K>
@@ -1426,7 +1425,7 @@ __global__ __launch_bounds__(256) void had_left_kernel(const float* __restrict__
 template <int K>
 __global__ __launch_bounds__(kFwdThreads) void ldlq_chain_kernel(
     const float* __restrict__ W, const float* __restrict__ Lq, int k, int n, int jc0, int tnl,
-    const uint16_t* __restrict__ lut16, int pivot, int n1, uint8_t* __restrict__ bp,
+    const float* __restrict__ lut, int pivot, int n1, uint8_t* __restrict__ bp,
     float* __restrict__ xbuf, float* __restrict__ hatW, float* __restrict__ Eq,
     int32_t* __restrict__ states, int16_t* __restrict__ trellis, uint32_t* __restrict__ flags,
     int32_t* __restrict__ counter, uint32_t epoch, int spin_limit, uint32_t* __restrict__ err,
@@ -1594,7 +1593,7 @@ __global__ __launch_bounds__(kFwdThreads) void ldlq_chain_kernel(
             const int nst = pass ? kSteps : n1, lo = pass ? 0 : pivot;
             if (tid == 0) sm.ovs[0] = pass ? (cur >> K) : -1;
             int tidv = tid;
-            const uint16_t* lutv = lut16;
+            const float* lutv = lut;
             asm volatile("" : "+v"(tidv));
             asm volatile("" : "+s"(lutv));
             fwd_run<K, 1>(sm, xs, kSteps, kSteps, 0, 1, lutv, pass ? 0 : pivot, nst, lo,
@@ -1612,7 +1611,7 @@ __global__ __launch_bounds__(kFwdThreads) void ldlq_chain_kernel(
             const int s = st[tid];
             const int pe = tc_perm(tid);
             const size_t g = (size_t)(16 * i + (pe >> 4)) * n + 16 * j + (pe & 15);
-            const float w = (float)__builtin_bit_cast(_Float16, lut16[s]);
+            const float w = lut[s];
             hatW[g] = w;
             const int m = 16 * i + (pe >> 4);                 // E in the quad layout
             Eq[(size_t)j * 16 * k + (size_t)(m >> 2) * 64 + 4 * (pe & 15) + (m & 3)] = W[g] - w;
@@ -1658,7 +1657,7 @@ constexpr int max_group() {
 template <int K>
 struct FwdL {
     static hipError_t run(const float* X, int xstride, int xlen, int nseq,
-                          const uint16_t* lut16, int roll, int nsteps, int store_lo,
+                          const float* lut, int roll, int nsteps, int store_lo,
                           const int32_t* ov_in, void* bp, int32_t* send, uint32_t* err,
                           int group, hipStream_t s) {
         const int T = group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 ? 4 : 8;
@@ -1666,22 +1665,22 @@ struct FwdL {
         const int nwg = (nseq + T - 1) / T;
         if (T == 1)
             hipLaunchKernelGGL((fwd_kernel<K, 1>), dim3(nwg), dim3(kFwdThreads), 0, s, X,
-                               xstride, xlen, nseq, lut16, roll, nsteps, store_lo, ov_in,
+                               xstride, xlen, nseq, lut, roll, nsteps, store_lo, ov_in,
                                (uint8_t*)bp, send, err);
         else if constexpr (max_group<K>() >= 2) {
             if (T == 2)
                 hipLaunchKernelGGL((fwd_kernel<K, 2>), dim3(nwg), dim3(kFwdThreads), 0, s,
-                                   X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo,
+                                   X, xstride, xlen, nseq, lut, roll, nsteps, store_lo,
                                    ov_in,
                                    (uint8_t*)bp, send, err);
             else if constexpr (max_group<K>() >= 4) {
                 if (T == 4)
                     hipLaunchKernelGGL((fwd_kernel<K, 4>), dim3(nwg), dim3(kFwdThreads), 0, s,
-                                       X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo,
+                                       X, xstride, xlen, nseq, lut, roll, nsteps, store_lo,
                                        ov_in, (uint8_t*)bp, send, err);
                 else if constexpr (max_group<K>() >= 8)
                     hipLaunchKernelGGL((fwd_kernel<K, 8>), dim3(nwg), dim3(kFwdThreads), 0, s,
-                                       X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo,
+                                       X, xstride, xlen, nseq, lut, roll, nsteps, store_lo,
                                        ov_in, (uint8_t*)bp, send, err);
             }
         }
@@ -1693,10 +1692,10 @@ struct FwdL {
 template <>
 struct FwdL<3> {
     static hipError_t run(const float* X, int xstride, int xlen, int nseq,
-                          const uint16_t* lut16, int roll, int nsteps, int store_lo,
+                          const float* lut, int roll, int nsteps, int store_lo,
                           const int32_t* ov_in, void* bp, int32_t* send, uint32_t* err,
                           int group, hipStream_t s) {
-        return launch_forward_k3(X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo, ov_in,
+        return launch_forward_k3(X, xstride, xlen, nseq, lut, roll, nsteps, store_lo, ov_in,
                                  bp, send, err, group, s);
     }
 };
@@ -1717,7 +1716,7 @@ struct GroupSel {
 template <int K>
 struct FwdDeferL {
     static hipError_t run(const float* X, int xstride, int xlen, int nseq,
-                          const uint16_t* lut16, int roll, int nsteps, int store_lo,
+                          const float* lut, int roll, int nsteps, int store_lo,
                           const int32_t* ov_in, void* bm, int32_t* send, uint32_t* err,
                           int group, hipStream_t s) {
         if constexpr (K < 4) {
@@ -1729,20 +1728,20 @@ struct FwdDeferL {
             float* b = (float*)bm;
             if (T == 1)
                 hipLaunchKernelGGL((fwd_defer_kernel<K, 1>), dim3(nwg), dim3(kFwdThreads), 0, s,
-                                   X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo, ov_in,
+                                   X, xstride, xlen, nseq, lut, roll, nsteps, store_lo, ov_in,
                                    b, send, err);
             else if (T == 2)
                 hipLaunchKernelGGL((fwd_defer_kernel<K, 2>), dim3(nwg), dim3(kFwdThreads), 0, s,
-                                   X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo, ov_in,
+                                   X, xstride, xlen, nseq, lut, roll, nsteps, store_lo, ov_in,
                                    b, send, err);
             else if constexpr (max_group<K>() >= 4) {
                 if (T == 4)
                     hipLaunchKernelGGL((fwd_defer_kernel<K, 4>), dim3(nwg), dim3(kFwdThreads),
-                                       0, s, X, xstride, xlen, nseq, lut16, roll, nsteps,
+                                       0, s, X, xstride, xlen, nseq, lut, roll, nsteps,
                                        store_lo, ov_in, b, send, err);
                 else if constexpr (max_group<K>() >= 8)
                     hipLaunchKernelGGL((fwd_defer_kernel<K, 8>), dim3(nwg), dim3(kFwdThreads),
-                                       0, s, X, xstride, xlen, nseq, lut16, roll, nsteps,
+                                       0, s, X, xstride, xlen, nseq, lut, roll, nsteps,
                                        store_lo, ov_in, b, send, err);
             }
             return hipGetLastError();
@@ -1753,7 +1752,7 @@ struct FwdDeferL {
 template <int K>
 struct TbDeferL {
     static hipError_t run(const void* bm, const float* X, int xstride, int xlen, int roll,
-                          const uint16_t* lut16, int nseq, const int32_t* send,
+                          const float* lut, int nseq, const int32_t* send,
                           const int32_t* ov_in, int nsteps, int stop, int shift, int32_t* sout,
                           int32_t* states, int16_t* trellis, hipStream_t s) {
         if constexpr (K < 4) {
@@ -1761,7 +1760,7 @@ struct TbDeferL {
         } else {
             hipLaunchKernelGGL(tb_defer_kernel<K>, dim3((nseq + kTbLaneSeqs - 1) / kTbLaneSeqs),
                                dim3(kTbLaneSeqs), 0, s, (const float*)bm, X, xstride, xlen, roll,
-                               lut16, nseq, send, ov_in, nsteps, stop, shift, sout, states,
+                               lut, nseq, send, ov_in, nsteps, stop, shift, sout, states,
                                trellis);
             return hipGetLastError();
         }
@@ -1783,13 +1782,13 @@ struct DeferBytes {
 
 template <int K>
 struct FusedL {
-    static hipError_t run(const float* X, int nseq, const uint16_t* lut16, int pivot, int n1,
+    static hipError_t run(const float* X, int nseq, const float* lut, int pivot, int n1,
                           void* bp, int32_t* send, int32_t* ovbuf, uint32_t* flags,
                           int32_t* counter, uint32_t epoch, int spin_limit, uint32_t* err,
                           hipStream_t s) {
         hipLaunchKernelGGL(reset_counter_kernel, dim3(1), dim3(1), 0, s, counter);
         hipLaunchKernelGGL(tailbite_fused_kernel<K>, dim3(2 * nseq), dim3(kFwdThreads), 0, s,
-                           X, nseq, lut16, pivot, n1, (uint8_t*)bp, send, ovbuf, flags,
+                           X, nseq, lut, pivot, n1, (uint8_t*)bp, send, ovbuf, flags,
                            counter, epoch, spin_limit, err);
         return hipGetLastError();
     }
@@ -1798,13 +1797,13 @@ struct FusedL {
 template <int K>
 struct ChainL {
     static hipError_t run(const float* W, const float* Lq, int k, int n, int jc0, int tnl,
-                          const uint16_t* lut16, int pivot, int n1, void* bp, int nwg,
+                          const float* lut, int pivot, int n1, void* bp, int nwg,
                           float* xbuf, int xdump, float* hatW, float* Eq, int32_t* states,
                           int16_t* trellis, uint32_t* flags, int32_t* counter, uint32_t epoch,
                           int spin_limit, uint32_t* err, int pbuf, hipStream_t s) {
         hipLaunchKernelGGL(reset_counter_kernel, dim3(1), dim3(1), 0, s, counter);
         hipLaunchKernelGGL(ldlq_chain_kernel<K>, dim3(nwg), dim3(kFwdThreads), 0, s, W, Lq, k,
-                           n, jc0, tnl, lut16, pivot, n1, (uint8_t*)bp, xbuf, hatW, Eq, states,
+                           n, jc0, tnl, lut, pivot, n1, (uint8_t*)bp, xbuf, hatW, Eq, states,
                            trellis, flags, counter, epoch, spin_limit, err, xdump, pbuf);
         return hipGetLastError();
     }
@@ -1830,9 +1829,9 @@ struct TbL {
 
 template <int K>
 struct DecL {
-    static hipError_t run(const int16_t* tr, int tk, int tn, const uint16_t* lut16,
+    static hipError_t run(const int16_t* tr, int tk, int tn, const float* lut,
                           float* of, uint16_t* oh, hipStream_t s) {
-        hipLaunchKernelGGL(decode_kernel<K>, dim3(tk * tn), dim3(256), 0, s, tr, tn, lut16,
+        hipLaunchKernelGGL(decode_kernel<K>, dim3(tk * tn), dim3(256), 0, s, tr, tn, lut,
                            of, oh);
         return hipGetLastError();
     }
@@ -1866,10 +1865,10 @@ struct StepBytes {
 
 #ifdef XTQ_FWD_K3_TU
 hipError_t launch_forward_k3(const float* X, int xstride, int xlen, int nseq,
-                             const uint16_t* lut16, int roll, int nsteps, int store_lo,
+                             const float* lut, int roll, int nsteps, int store_lo,
                              const int32_t* ov_in, void* bp, int32_t* send, uint32_t* err,
                              int group, hipStream_t stream) {
-    return FwdL<3>::run(X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo, ov_in, bp, send,
+    return FwdL<3>::run(X, xstride, xlen, nseq, lut, roll, nsteps, store_lo, ov_in, bp, send,
                         err, group, stream);
 }
 #else
@@ -1886,25 +1885,25 @@ int forward_group(int K, int nseq, int ncu) {
 }
 
 hipError_t launch_forward(int K, const float* X, int xstride, int xlen, int nseq,
-                          const uint16_t* lut16, int roll, int nsteps, int store_lo,
+                          const float* lut, int roll, int nsteps, int store_lo,
                           const int32_t* ov_in, void* bp, int32_t* send, uint32_t* err,
                           int group, hipStream_t stream) {
     if (nseq <= 0) return hipSuccess;
     if (xlen < 1 || xlen > kSteps || nsteps < 1 || nsteps > kSteps || roll < 0 ||
         roll >= xlen || (roll != 0 && xlen != kSteps) || (roll == 0 && nsteps > xlen))
         return hipErrorInvalidValue;
-    return dispatch_k<FwdL>(K, X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo, ov_in,
+    return dispatch_k<FwdL>(K, X, xstride, xlen, nseq, lut, roll, nsteps, store_lo, ov_in,
                             bp, send, err, group, stream);
 }
 
-hipError_t launch_tailbite_fused(int K, const float* X, int nseq, const uint16_t* lut16,
+hipError_t launch_tailbite_fused(int K, const float* X, int nseq, const float* lut,
                                  int pivot, int n1, void* bp, int32_t* send, int32_t* ovbuf,
                                  uint32_t* flags, int32_t* counter, uint32_t epoch,
                                  int spin_limit, uint32_t* err, hipStream_t stream) {
     if (nseq <= 0) return hipSuccess;
     if (pivot < 0 || pivot >= kSteps || n1 <= pivot || n1 > kSteps || spin_limit < 1)
         return hipErrorInvalidValue;
-    return dispatch_k<FusedL>(K, X, nseq, lut16, pivot, n1, bp, send, ovbuf, flags, counter,
+    return dispatch_k<FusedL>(K, X, nseq, lut, pivot, n1, bp, send, ovbuf, flags, counter,
                               epoch, spin_limit, err, stream);
 }
 
@@ -1926,7 +1925,7 @@ hipError_t launch_lfac_quads(const float* L, int k, float* Lq, hipStream_t strea
 }
 
 hipError_t launch_ldlq_chain(int K, const float* W, const float* Lq, int k, int n, int jc0,
-                            int tnl, const uint16_t* lut16, int pivot, int n1, void* bp,
+                            int tnl, const float* lut, int pivot, int n1, void* bp,
                             int nwg, float* xbuf, int xdump, float* hatW, float* Eq,
                             int32_t* states, int16_t* trellis, uint32_t* flags,
                             int32_t* counter, uint32_t epoch, int spin_limit, uint32_t* err,
@@ -1936,7 +1935,7 @@ hipError_t launch_ldlq_chain(int K, const float* W, const float* Lq, int k, int 
         n1 <= pivot || n1 > kSteps || nwg < 1 || spin_limit < 1 || buf_cols < 16 ||
         buf_cols % 16)
         return hipErrorInvalidValue;
-    return dispatch_k<ChainL>(K, W, Lq, k, n, jc0, tnl, lut16, pivot, n1, bp, nwg, xbuf, xdump,
+    return dispatch_k<ChainL>(K, W, Lq, k, n, jc0, tnl, lut, pivot, n1, bp, nwg, xbuf, xdump,
                               hatW, Eq, states, trellis, flags, counter, epoch, spin_limit, err,
                               buf_cols / 16, stream);
 }
@@ -1951,10 +1950,10 @@ hipError_t launch_traceback(int K, const void* bp, int nseq, const int32_t* send
                            lanes, stream);
 }
 
-hipError_t launch_decode(int K, const int16_t* trellis, int tk, int tn, const uint16_t* lut16,
+hipError_t launch_decode(int K, const int16_t* trellis, int tk, int tn, const float* lut,
                          float* out_f32, uint16_t* out_f16, hipStream_t stream) {
     if (tk <= 0 || tn <= 0) return hipSuccess;
-    return dispatch_k<DecL>(K, trellis, tk, tn, lut16, out_f32, out_f16, stream);
+    return dispatch_k<DecL>(K, trellis, tk, tn, lut, out_f32, out_f16, stream);
 }
 
 hipError_t launch_pack(int K, const int32_t* states, int nt, int16_t* trellis,
@@ -1976,7 +1975,7 @@ size_t defer_tile_bytes(int K) {
 }
 
 hipError_t launch_forward_defer(int K, const float* X, int xstride, int xlen, int nseq,
-                                const uint16_t* lut16, int roll, int nsteps, int store_lo,
+                                const float* lut, int roll, int nsteps, int store_lo,
                                 const int32_t* ov_in, void* bm, int32_t* send, uint32_t* err,
                                 int group, hipStream_t stream) {
     if (nseq <= 0) return hipSuccess;
@@ -1984,12 +1983,12 @@ hipError_t launch_forward_defer(int K, const float* X, int xstride, int xlen, in
         roll >= xlen || (roll != 0 && xlen != kSteps) || (roll == 0 && nsteps > xlen) ||
         store_lo < 0)
         return hipErrorInvalidValue;
-    return dispatch_k<FwdDeferL>(K, X, xstride, xlen, nseq, lut16, roll, nsteps, store_lo,
+    return dispatch_k<FwdDeferL>(K, X, xstride, xlen, nseq, lut, roll, nsteps, store_lo,
                                  ov_in, bm, send, err, group, stream);
 }
 
 hipError_t launch_traceback_defer(int K, const void* bm, const float* X, int xstride, int xlen,
-                                  int roll, const uint16_t* lut16, int nseq,
+                                  int roll, const float* lut, int nseq,
                                   const int32_t* send, const int32_t* ov_in, int nsteps,
                                   int stop, int shift, int32_t* sout, int32_t* states,
                                   int16_t* trellis, hipStream_t stream) {
@@ -1997,7 +1996,7 @@ hipError_t launch_traceback_defer(int K, const void* bm, const float* X, int xst
     if (nsteps < 1 || nsteps > kSteps || stop < 0 || stop >= nsteps || roll < 0 ||
         roll >= xlen || xlen < 1 || xlen > kSteps)
         return hipErrorInvalidValue;
-    return dispatch_k<TbDeferL>(K, bm, X, xstride, xlen, roll, lut16, nseq, send, ov_in,
+    return dispatch_k<TbDeferL>(K, bm, X, xstride, xlen, roll, lut, nseq, send, ov_in,
                                 nsteps, stop, shift, sout, states, trellis, stream);
 }
 

@@ -23,7 +23,8 @@ _LIB = None
 
 # Codebook names accepted by the library (fp16-exact V=1 codes).
 CODE_NAMES = {"exl3_mul1": "mul1", "exl3_3inst": "3inst", "exl3_mcg": "mcg",
-              "mul1": "mul1", "3inst": "3inst", "mcg": "mcg"}
+              "qtip_1mad": "1mad",
+              "mul1": "mul1", "3inst": "3inst", "mcg": "mcg", "1mad": "1mad"}
 
 
 class HipViterbiError(RuntimeError):

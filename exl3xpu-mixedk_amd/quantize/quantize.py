@@ -93,15 +93,15 @@ def _kernel_code(lut: torch.Tensor, L: int) -> str:
     if L != 16:
         raise NotImplementedError("the HIP trellis kernels use the 16-bit state (L=16)")
     lut = lut.detach().float().reshape(-1).cpu()
-    for name in ("exl3_mul1", "exl3_3inst", "exl3_mcg"):
+    for name in ("exl3_mul1", "exl3_3inst", "exl3_mcg", "qtip_1mad"):
         ref = _LUT_IDS.get(name)
         if ref is None:
             ref = _LUT_IDS[name] = get_lut(name, 16)
         if lut.shape == ref.shape and torch.equal(lut, ref):
             return name
     raise NotImplementedError(
-        "the HIP trellis kernels run the fp16-exact EXL3 codes exl3_mul1, exl3_3inst and "
-        "exl3_mcg; this decode table is none of them")
+        "the HIP trellis kernels run the V=1 codes exl3_mul1, exl3_3inst, exl3_mcg and "
+        "qtip_1mad; this decode table is none of them")
 
 
 # ------------------------------------------------------------ tile layout

@@ -28,7 +28,8 @@
  *      exceed XTQ_VIT_DEV_MAXBYTES
  *   6  nseq <= 0, or nseq > XTQ_VIT_MAXSEQ on the host-pointer entries;
  *      bad shapes on the device entries
- *   8  unsupported code (e.g. "ih2x2"; only fp16-exact V=1 codebooks run)
+ *   8  unsupported code (e.g. "ih2x2"; the V=1 codebooks run: "mul1",
+ *      "3inst", "mcg" and "1mad")
  *   9  K outside 2..7 (or K != 4 for the K=4-only reference codes)
  *  10  pivot outside [0,256), or margin < 0 on the entries the reference
  *      has no counterpart for (xtq_vit_run treats margin < 0 as 0, as the
@@ -104,7 +105,9 @@ XTQ_API int xtq_vit_run(const float* X, int nseq, const char* code, int margin, 
 /*
  * K-aware host-pointer variant of xtq_vit_run (no reference counterpart: the
  * reference kernel is K=4 only, viterbi_esimd.cpp:83,352; the torch path it
- * generalises is quantize.py:323-354).  code: "mul1", "3inst" or "mcg".
+ * generalises is quantize.py:323-354).  code: "mul1", "3inst", "mcg" (the
+ * EXL3 codes, fp16 values) or "1mad" (QTIP's 1MAD code, fp32 values); the
+ * exl3_/qtip_ prefixed names of quantize.py are accepted too.
  */
 XTQ_API int xtq_vit_run_k(const float* X, int nseq, int K, const char* code, int margin,
                   int pivot, int32_t* out);
@@ -235,7 +238,9 @@ XTQ_API int xtq_vit_viterbi_dev(const float* dX, int nseq, int T, int K, const c
  * (quantize.py:405-415) and of exl3xpu's reconstruct (patch 0001:60-75).
  *   d_trellis [tk][tn][16K] int16 device
  *   d_out_f32 [16tk][16tn] fp32 device, or NULL
- *   d_out_f16 [16tk][16tn] fp16 (bit patterns) device, or NULL
+ *   d_out_f16 [16tk][16tn] fp16 (bit patterns) device, or NULL: the table
+ *             value rounded to fp16 (exact for the EXL3 codes; "1mad"'s fp32
+ *             values round)
  * Stream-ordered: returns once the kernel is enqueued on `stream` (as do
  * the pack and unpack entries below).
  */

@@ -7,6 +7,7 @@ the GPU host):
     python tests/golden/make_golden.py /root/reference/quantize
     python tests/golden/make_golden.py /root/reference/quantize --ties
     python tests/golden/make_golden.py /root/reference/quantize --mid
+    python tests/golden/make_golden.py /root/reference/quantize --codes
 
 It imports the reference quantizer module (quantize/quantize.py) on CPU and
 records input/output vectors for the functions that closed forms, invariants
@@ -23,6 +24,12 @@ and brute force cannot pin:
 --ties writes ties.npz alone: quantize_seq_tailbite on 24 sequences per K
 whose results hinge on exact cost ties (six kinds, tie_forcing_inputs) at four
 pivot/margin pairs, and viterbi() pinned and back_from runs on them.
+--codes writes codes.npz alone: the reference's decode tables of the other
+V=1 codes (exl3_3inst, exl3_mcg, qtip_1mad; quantize.py:56-97) as SHA-256
+digests of their fp32 bytes with their first 64 entries, and
+quantize_seq_tailbite states with the qtip_1mad table on Gaussian and
+tie-forcing sequences (the six kinds of --ties) at K = 2, 4, 7, margins
+{0, 16}.
 --mid writes e2e_mid.npz alone: quantize_linear with BlockLDLQ on a
 1024x1024 weight (4,096 tiles, 64 blocks of feedback) against the Hessian
 H[i][j] = 2^-|i-j| (exact in fp32), at K=4 and at K=5 with channel scales:
@@ -123,6 +130,33 @@ def main_ties(refdir: str):
         data[f"VB_K{K}"] = xq.viterbi(Xt[:200], lut, K, 16, back_from=60).numpy().astype(np.int32)
         print(f"  ties K={K} done {time.time() - t0:.1f}s", flush=True)
     np.savez_compressed(os.path.join(OUT, "ties.npz"), **data)
+
+
+def main_codes(refdir: str):
+    sys.path.insert(0, refdir)
+    import quantize as xq  # the reference module, CPU only
+    torch.set_num_threads(8)
+    data = {}
+    for name in ("exl3_3inst", "exl3_mcg", "qtip_1mad"):
+        t = xq.get_lut(name, 16).numpy().astype(np.float32)
+        data[f"sha256_{name}"] = np.frombuffer(hashlib.sha256(t.tobytes()).digest(),
+                                               dtype=np.uint8)
+        data[f"head_{name}"] = t[:64].copy()
+    lut = xq.get_lut("qtip_1mad", 16)
+    lut_np = lut.numpy().astype(np.float32)
+    rng = np.random.default_rng(20261203)
+    t0 = time.time()
+    for K in (2, 4, 7):
+        g = rng.standard_normal((2, 256)).astype(np.float32)
+        ties = tie_forcing_inputs(lut_np, rng, 6)
+        X = np.concatenate([g, ties], 0)                 # [8, 256]
+        data[f"mad_X_K{K}"] = X
+        Xt = torch.from_numpy(X.T.copy())
+        for p, m in ((128, 0), (147, 16)):
+            st = xq.quantize_seq_tailbite(Xt, lut, K, 16, pivot=p, margin=m)
+            data[f"mad_S_K{K}_m{m}_p{p}"] = st.t().numpy().astype(np.int32)
+        print(f"  qtip_1mad K={K} done {time.time() - t0:.1f}s", flush=True)
+    np.savez_compressed(os.path.join(OUT, "codes.npz"), **data)
 
 
 def kms_hessian(d: int) -> np.ndarray:
@@ -273,5 +307,7 @@ if __name__ == "__main__":
         main_ties(ref)
     elif "--mid" in sys.argv[1:]:
         main_mid(ref)
+    elif "--codes" in sys.argv[1:]:
+        main_codes(ref)
     else:
         main(ref)

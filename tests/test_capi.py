@@ -45,6 +45,13 @@ def test_lut_export(lib):
     assert lib.xtq_vit_get_lut(b"mul1", out.ctypes.data_as(ctypes.c_void_p)) == 0
     np.testing.assert_array_equal(out, load_golden("lut_mul1.npz")["lut"])
     assert lib.xtq_vit_get_lut(b"ih2x2", out.ctypes.data_as(ctypes.c_void_p)) == 8
+    # the other codes' device tables equal the reference's get_lut tables
+    import hashlib
+    g = load_golden("codes.npz")
+    for short, name in (("3inst", "exl3_3inst"), ("mcg", "exl3_mcg"), ("1mad", "qtip_1mad"),
+                        ("qtip_1mad", "qtip_1mad")):
+        assert lib.xtq_vit_get_lut(short.encode(), out.ctypes.data_as(ctypes.c_void_p)) == 0
+        assert hashlib.sha256(out.tobytes()).digest() == g[f"sha256_{name}"].tobytes(), short
 
 
 def test_status_codes_without_device(lib):

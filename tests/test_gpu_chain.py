@@ -135,11 +135,13 @@ def test_chain_vs_oracle(xq, hb, oracle_mod, mul1_lut, K, k, n, pivot, margin):
     np.testing.assert_array_equal(hatW.numpy(), oracle_mod.decode(tr.numpy(), mul1_lut, K))
 
 
-@pytest.mark.parametrize("name,short,K", [("exl3_3inst", "3inst", 4), ("exl3_mcg", "mcg", 6)])
+@pytest.mark.parametrize("name,short,K", [("exl3_3inst", "3inst", 4), ("exl3_mcg", "mcg", 6),
+                                          ("qtip_1mad", "1mad", 5)])
 def test_chain_other_codebooks(xq, hb, oracle_mod, name, short, K):
-    """The 3inst and mcg codebooks (fp16-exact, quantize.py:64-71) through the
-    chain: targets against the fp64 formula, states and packing against the
-    oracle with that codebook's table, decode with the same table."""
+    """The 3inst and mcg codebooks (fp16-exact, quantize.py:64-71) and QTIP's
+    1MAD code (fp32 values, quantize.py:82-86) through the chain: targets
+    against the fp64 formula, states and packing against the oracle with that
+    codebook's table, decode with the same table."""
     g = torch.Generator().manual_seed(60 + K)
     W = torch.randn(96, 64, generator=g)
     L = _lfac(xq, 96, K)
@@ -476,6 +478,21 @@ def test_buffer_width_rounds_like_reference(xq, given, runs_as):
     assert torch.equal(sg, sw) and torch.equal(hg, hw)
     hb_, sb = xq.ldlq_viterbi(Wq, Lf, lut, 4, 16, margin=0, buf_cols=given, schedule="block")
     assert torch.equal(sb, sw.cpu()) and torch.equal(hb_, hw.cpu())
+
+
+def test_quantize_linear_1mad_chain_equals_block(xq):
+    """quantize_linear with code="qtip_1mad" on the GPU (column chains) equals
+    the reference's CPU block schedule bit for bit: trellis and W_hat."""
+    import workloads as wl
+    g = torch.Generator().manual_seed(21)
+    W = 0.02 * torch.randn(128, 256, generator=g)
+    H = wl.ar1_gram(256, 512, 0.5, 21)
+    print("case quantize_linear 128x256 qtip_1mad K=3 chain vs CPU", flush=True)
+    rg = xq.quantize_linear(W.cuda(), H.cuda(), code="qtip_1mad", K=3, device="cuda",
+                            reference_arithmetic=True)
+    rc = xq.quantize_linear(W, H, code="qtip_1mad", K=3, device="cpu")
+    assert torch.equal(rg["trellis"], rc["trellis"])
+    assert torch.equal(rg["W_hat"], rc["W_hat"])
 
 
 def test_chain_factor_over_2g_elements(hb, oracle_mod, mul1_lut):

@@ -26,6 +26,12 @@ def hb():
     return hip_backend
 
 
+@pytest.fixture(scope="module")
+def xq(hb):
+    import quantize
+    return quantize
+
+
 def _run(hb, X: np.ndarray, K: int, pivot: int, margin: int, trellis=False):
     Xd = torch.from_numpy(np.ascontiguousarray(X, dtype=np.float32)).cuda()
     st, tr = hb.tailbite(Xd, K, pivot, margin, states=True, trellis=trellis)
@@ -420,6 +426,65 @@ def test_other_codebooks(hb, oracle_mod):
         Xd = torch.from_numpy(X).cuda()
         st, _ = hb.tailbite(Xd, 3, 128, 0, code=short)
         np.testing.assert_array_equal(st.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("group", ("1", "2", "4", "8", "fused", "d4"))
+def test_1mad_vs_reference_golden(hb, oracle_mod, group, monkeypatch):
+    """QTIP's 1MAD code -- fp32 table values, (bytesum - 510) / 147.8, not
+    fp16-exact -- through every forward path: the reference's own states on
+    Gaussian and tie-forcing targets (codes.npz) at K = 2, 4, 7, and the
+    oracle with that table on random batches; the packed trellis too."""
+    monkeypatch.setenv("XTQ_VIT_DEFER", "1" if group.startswith("d") else "0")
+    if group == "fused":
+        monkeypatch.setenv("XTQ_VIT_FUSED", "1")
+    else:
+        monkeypatch.setenv("XTQ_VIT_FUSED", "0")
+        monkeypatch.setenv("XTQ_VIT_GROUP", group.lstrip("d"))
+    g = load_golden("codes.npz")
+    lut = oracle_mod.code_lut("qtip_1mad")
+    rng = np.random.default_rng(77)
+    for K in (2, 4, 7):
+        if group.startswith("d") and K < 4:
+            continue
+        X = g[f"mad_X_K{K}"]
+        Xd = torch.from_numpy(X).cuda()
+        for p, m in ((128, 0), (147, 16)):
+            print(f"case 1mad K={K} group={group} pivot={p} margin={m}", flush=True)
+            st, tr = hb.tailbite(Xd, K, p, m, code="1mad", trellis=True)
+            want = g[f"mad_S_K{K}_m{m}_p{p}"]
+            np.testing.assert_array_equal(st.cpu().numpy(), want)
+            np.testing.assert_array_equal(tr.cpu().numpy(), oracle_mod.pack(want, K))
+        Xr = rng.standard_normal((9, 256)).astype(np.float32)
+        Xr[1] = lut[rng.integers(0, 65536, 256)]
+        st, _ = hb.tailbite(torch.from_numpy(Xr).cuda(), K, 5, 16, code="1mad")
+        np.testing.assert_array_equal(st.cpu().numpy(),
+                                      oracle_mod.tailbite(Xr, lut, K, 16, pivot=5, margin=16))
+
+
+@pytest.mark.parametrize("K", (2, 4))
+@pytest.mark.parametrize("code", ("exl3_mul1", "qtip_1mad"))
+def test_gaussian_mse_on_gpu(xq, oracle_mod, code, K):
+    """The reference's rate-distortion check (test_quantize.py:183-202) on the
+    GPU: rms-matched Gaussian targets, 2,048 tiles through
+    quantize_seq_tailbite, MSE below 3 x 2^-2K, for both codes; the decode of
+    the states with the code's fp32 table matches the oracle's decode."""
+    torch.manual_seed(3)
+    lut = xq.get_lut(code, 16)
+    lut_rms = lut.double().square().mean().sqrt().float()
+    X = torch.randn(256, 2048)
+    X = X / X.square().mean().sqrt() * lut_rms
+    print(f"case gaussian mse {code} K={K}", flush=True)
+    st = xq.quantize_seq_tailbite(X.cuda(), lut.cuda(), K, 16)
+    dec = lut.cuda()[st].t().contiguous().flatten()
+    mse = float((dec - X.cuda().t().reshape(-1)).square().mean() / X.square().mean())
+    print(f"{code} K={K}: mse {mse:.5f} vs bound {2.0 ** (-2 * K):.5f}", flush=True)
+    assert mse < 3.0 * 2.0 ** (-2 * K)
+    short = {"exl3_mul1": "mul1", "qtip_1mad": "1mad"}[code]
+    st32 = st.t().contiguous().to(torch.int32)[:32]
+    tr = xq._hb.pack(st32, K).view(2, 16, 16 * K)
+    np.testing.assert_array_equal(
+        xq._hb.decode(tr, K, code=short).cpu().numpy(),
+        oracle_mod.decode(tr.cpu().numpy(), oracle_mod.code_lut(code), K))
 
 
 def test_verify_viterbi_readme_case(hb, oracle_mod, mul1_lut):

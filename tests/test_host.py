@@ -123,8 +123,8 @@ def test_unsupported_variants_raise(xq):
         xq.viterbi(X, lut, 4, 16, V=2)
     with pytest.raises(NotImplementedError):
         xq.quantize_seq_tailbite(X, xq.get_lut("exl3_mul1", 12), 4, 12)
-    with pytest.raises(NotImplementedError):
-        xq.quantize_seq_tailbite(X, xq.get_lut("qtip_1mad"), 4, 16)
+    with pytest.raises(NotImplementedError):        # a table of no supported code
+        xq.quantize_seq_tailbite(X, xq.get_lut("qtip_1mad") * 2, 4, 16)
     with pytest.raises(NotImplementedError):
         xq.quantize_seq_tailbite(torch.zeros(128, 2), lut, 4, 16)
     with pytest.raises(ValueError):

@@ -126,6 +126,30 @@ def test_oracle_vs_reference_golden(oracle_mod, mul1_lut, K):
 TIE_CASES = ((128, 0), (147, 16), (0, 0), (255, 16))
 
 
+@pytest.mark.parametrize("name", ("exl3_3inst", "exl3_mcg", "qtip_1mad"))
+def test_other_code_tables_golden(oracle_mod, name):
+    """The other V=1 decode tables restated by the oracle equal the
+    reference's get_lut tables byte for byte (quantize.py:56-97)."""
+    import hashlib
+    g = load_golden("codes.npz")
+    t = oracle_mod.code_lut(name)
+    assert t.dtype == np.float32 and t.shape == (65536,)
+    np.testing.assert_array_equal(t[:64], g[f"head_{name}"])
+    assert hashlib.sha256(t.tobytes()).digest() == g[f"sha256_{name}"].tobytes()
+
+
+@pytest.mark.parametrize("K", (2, 4, 7))
+def test_oracle_1mad_vs_reference_golden(oracle_mod, K):
+    """Tail-bite with the QTIP 1MAD table (fp32 values, not fp16-exact) on
+    Gaussian and tie-forcing targets equals the reference's states."""
+    g = load_golden("codes.npz")
+    lut = oracle_mod.code_lut("qtip_1mad")
+    X = g[f"mad_X_K{K}"]
+    for p, m in ((128, 0), (147, 16)):
+        np.testing.assert_array_equal(oracle_mod.tailbite(X, lut, K, 16, pivot=p, margin=m),
+                                      g[f"mad_S_K{K}_m{m}_p{p}"], err_msg=f"p={p} m={m}")
+
+
 @pytest.mark.parametrize("K", range(2, 8))
 def test_oracle_vs_reference_ties(oracle_mod, mul1_lut, K):
     """The reference's outputs on 24 tie-forcing sequences per K (ties.npz):
@@ -241,14 +265,17 @@ def test_tailbite_wrap_invariant(oracle_mod, mul1_lut, K):
 
 
 @pytest.mark.parametrize("K", (2, 4))
-def test_gaussian_mse_bound(oracle_mod, mul1_lut, K):
-    """MSE < 3 * 2^-2K on rms-matched Gaussian targets (test_quantize.py:183-202)."""
+@pytest.mark.parametrize("code", ("exl3_mul1", "qtip_1mad"))
+def test_gaussian_mse_bound(oracle_mod, code, K):
+    """MSE < 3 * 2^-2K on rms-matched Gaussian targets, for both codes
+    (test_quantize.py:183-202)."""
+    lut = oracle_mod.code_lut(code)
     rng = np.random.default_rng(3)
     X = rng.standard_normal((16, 256)).astype(np.float32)
-    lut_rms = np.sqrt((mul1_lut.astype(np.float64) ** 2).mean())
+    lut_rms = np.sqrt((lut.astype(np.float64) ** 2).mean())
     X = (X / np.sqrt((X.astype(np.float64) ** 2).mean()) * lut_rms).astype(np.float32)
-    st = oracle_mod.tailbite(X, mul1_lut, K, 16)
-    mse = ((mul1_lut[st] - X) ** 2).mean() / (X ** 2).mean()
+    st = oracle_mod.tailbite(X, lut, K, 16)
+    mse = ((lut[st] - X) ** 2).mean() / (X ** 2).mean()
     assert mse < 3.0 * 2.0 ** (-2 * K)
 
 
