@@ -1158,6 +1158,19 @@ int xtq_had128_left_dev(const float* d_ht, const float* d_in, float* d_out, int 
     return 0;
 }
 
+int xtq_had128_right_dev(const float* d_h, const float* d_in, float* d_out, int rows, int cols,
+                         void* stream) {
+    if (!d_h || !d_in || !d_out) return 12;
+    if (d_in == d_out) return 12;
+    if (rows <= 0 || cols <= 0 || cols % 128 || (rows + 31) / 32 > 65535) return 6;
+    hipError_t e = xtq::launch_had_right(d_h, d_in, d_out, rows, cols, (hipStream_t)stream);
+    if (e != hipSuccess) {
+        fprintf(stderr, "xtq_vit had128: %s\n", hipGetErrorString(e));
+        return 4;
+    }
+    return 0;
+}
+
 int xtq_vit_get_lut(const char* code, float* out) {
     if (!out) return 12;
     Code c;

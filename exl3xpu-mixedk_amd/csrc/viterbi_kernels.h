@@ -96,6 +96,14 @@ hipError_t launch_lfac_quads(const float* L, int k, float* Lq, hipStream_t strea
 hipError_t launch_had_left(const float* ht, const float* in, float* out, int rows, int cols,
                            hipStream_t stream);
 
+// out = in @ blockdiag(h) for in, out [rows][cols] fp32 row-major (cols a
+// multiple of 128, in != out), h[t][c] the weight of input column t in
+// output column c: each output one fp32 fused multiply-add chain in
+// ascending order (the products and order of launch_had_left on the
+// transpose).
+hipError_t launch_had_right(const float* h, const float* in, float* out, int rows, int cols,
+                            hipStream_t stream);
+
 // The BlockLDLQ sweep of the column tiles jc0 .. jc0+tnl-1 of W [k][n]
 // (inner domain, row-major, k and n multiples of 16) as one persistent
 // launch of nwg workgroups over their column chains (see ldlq_chain_kernel).

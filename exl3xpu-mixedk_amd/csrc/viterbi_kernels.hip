@@ -526,12 +526,17 @@ __device__ __forceinline__ void fwd_run(
                         // this step's backpointer row: a wave-uniform base
                         // (SGPRs) plus a 32-bit lane offset, so the store
                         // takes the SGPR-base form and no 64-bit per-lane
-                        // address is carried across steps
+                        // address is carried across steps (the offset is
+                        // opaque here: hoisted out of the step loop, its
+                        // 64-bit extension was kept live there instead, and
+                        // spilled in the column-chain kernel)
                         gbyte_t* const bprow =
                             uniform_gptr(bp + ((size_t)q * kSlots + (size_t)i) * G::BPSTEP);
+                        uint32_t loff = G::HALF ? (uint32_t)jb : (uint32_t)(tl * G::UNIT);
+                        asm volatile("" : "+v"(loff));
                         if constexpr (G::HALF) {
                             if ((tl & 1) == 0)
-                                bprow[(uint32_t)jb] = (uint8_t)(key_lo(run[0]) & 0x7F);
+                                bprow[loff] = (uint8_t)(key_lo(run[0]) & 0x7F);
                         } else {
                             // Funnel-shift each group's K index bits (the low
                             // bits of its key tag) in from the top, one
@@ -543,8 +548,7 @@ __device__ __forceinline__ void fwd_run(
                             for (int c = 0; c < G::C; ++c)
                                 bits = __builtin_amdgcn_alignbit(key_lo(run[c]), bits, (uint32_t)K);
                             if constexpr (G::BITS < 32) bits >>= (32 - G::BITS);
-                            *(__attribute__((address_space(1))) unit_t*)(bprow +
-                                                                         (uint32_t)(tl * G::UNIT)) =
+                            *(__attribute__((address_space(1))) unit_t*)(bprow + loff) =
                                 (unit_t)bits;
                         }
                     }
@@ -1356,10 +1360,81 @@ __global__ __launch_bounds__(64) void pack_kernel(const int32_t* __restrict__ st
 // buffer b's chain in m order exactly.  A round covers 64 buffers (4 per
 // wave); the 256 partials of each buffer go to LDS and 256 threads fold
 // them into prod in buffer order.
-constexpr int kFbPrefetch = 2;     // feedback m-quads in flight per lane
+//
+// Feedback loads in flight per lane: one block of 16 rows (4 m-quads of L
+// and E).  A full round is bound by the matrix cores: 4 waves x 128
+// dependent 16x16x1 MFMAs per SIMD.
+constexpr int kFbBlk = 4;          // m-quads per block
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+
+// One wave's feedback chains of a round: block blk of the accumulator is
+// buffer bw + blk, and lane (blk, rc) feeds row rc of L and column rc of E
+// of that buffer, m-quad mq (4 consecutive m, one 16-byte load of each) at
+// byte offset off0 + 256 mq from the wave-uniform bases lb and eb; nqw
+// (wave-uniform) m-quads, kFbDepth of them in flight.  The four MFMAs of an
+// m-quad add rows m, m+1, m+2, m+3 in that order, so every accumulator is
+// one fused multiply-add chain over its buffer's rows in ascending order.
+// RAGGED: the lane's own buffer ends after nq <= nqw m-quads (block i's
+// partial buffer, or none); its loads past nq re-read its last valid m-quad
+// (every address stays inside the matrices) and the values are zeroed where
+// they are used, so the extra products leave the chain unchanged.  Zeroing
+// them at the load instead would make every load wait for itself.
+template <bool RAGGED>
+__device__ __forceinline__ v16f fb_chain(const gbyte_t* lb, const gbyte_t* eb, uint32_t off0,
+                                         int nq, int nqw) {
+    typedef __attribute__((address_space(1))) const v4f gv4_t;
+    const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
+    v16f acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+    // nqw is a whole number nb of blocks (m-quads of whole 16-row blocks)
+    const int nb = nqw / kFbBlk;
+    auto off = [&](int mq) -> uint32_t {
+        if constexpr (RAGGED) {
+            const int mc = mq < nq ? mq : (nq > 0 ? nq - 1 : 0);
+            return off0 + 256u * (uint32_t)mc;
+        } else {
+            return off0 + 256u * (uint32_t)mq;
+        }
+    };
+    v4f ra[kFbBlk], re[kFbBlk];
+    // m-quad mq into slot u; past the last block it re-reads the last one
+    // (never used), so that no load is conditional
+    auto load = [&](int u, int bb) __attribute__((always_inline)) {
+        const int bc = bb < nb ? bb : nb - 1;
+        ra[u] = *(gv4_t*)(lb + off(bc * kFbBlk + u));
+        re[u] = *(gv4_t*)(eb + off(bc * kFbBlk + u));
+    };
+    // A slot is refilled (with the same m-quad of the next block) right
+    // after its MFMAs have read it, into the same registers; the scheduling
+    // barriers keep each refill there (the compiler would otherwise sink
+    // the loads to the end of the block, next to their use).  Every path
+    // into the loop has the same loads outstanding, so each wait is for one
+    // slot only.
+#pragma unroll
+    for (int u = 0; u < kFbBlk; ++u) load(u, 0);
+    for (int bb = 0; bb < nb; ++bb) {
+#pragma unroll
+        for (int u = 0; u < kFbBlk; ++u) {
+            const int mq = bb * kFbBlk + u;
+            v4f a = ra[u], e = re[u];
+            if constexpr (RAGGED) {
+                a = mq < nq ? a : z;
+                e = mq < nq ? e : z;
+            }
+            acc = __builtin_amdgcn_mfma_f32_16x16x1f32(a.x, e.x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x1f32(a.y, e.y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x1f32(a.z, e.z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x1f32(a.w, e.w, acc, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            load(u, bb + 1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    return acc;
+}
 
 // Operand layout of the feedback ("quad layout"): a [k][n] matrix M is
 // stored per 16-column block b as a [k/4][16][4] array,
@@ -1420,6 +1495,54 @@ __global__ __launch_bounds__(256) void had_left_kernel(const float* __restrict__
 #pragma unroll
         for (int q = 0; q < 16; ++q) dst[(size_t)q * cols] = acc[q];
     }
+}
+
+// out[r][128b + c] = sum_{t=0..127} h[t][c] * in[r][128b + t] (had_right,
+// quantize.py:141-145) without a transpose: each output one fp32 fused
+// multiply-add chain over t ascending, from zero -- the products and the
+// order of had_left_kernel on the transpose, hence torch's CPU sgemm bits.
+// Wave: 8 rows x 64 columns (half of a 128-column block); the 8 inputs of a
+// step t are wave-uniform (scalar loads, 8 consecutive t per row at a time)
+// and the multipliers h[t][c] one coalesced row segment.  Workgroup: 4
+// waves, 32 rows.  (16 rows per wave with 4 steps per scalar load measured
+// 1.7x slower: twice the scalar loads per multiply-add.)
+constexpr int kHrRows = 8;                 // rows per wave
+constexpr int kHrT = 8;                    // steps per scalar load
+__global__ __launch_bounds__(256) void had_right_kernel(const float* __restrict__ h,
+                                                        const float* __restrict__ in,
+                                                        float* __restrict__ out, int rows,
+                                                        int cols) {
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), ln = threadIdx.x & 63;
+    const int b = blockIdx.x >> 1;                          // 128-column block
+    const int c = ((blockIdx.x & 1) << 6) + ln;             // column within the block
+    const int r0 = (blockIdx.y * 4 + wv) * kHrRows;
+    if (r0 >= rows) return;
+    const int nr = rows - r0 < kHrRows ? rows - r0 : kHrRows;   // wave-uniform
+    const float* src = in + (size_t)r0 * cols + 128 * b;
+    float acc[kHrRows];
+#pragma unroll
+    for (int q = 0; q < kHrRows; ++q) acc[q] = 0.0f;
+    if (nr == kHrRows) {
+        for (int t0 = 0; t0 < 128; t0 += kHrT) {
+#pragma unroll
+            for (int t = t0; t < t0 + kHrT; ++t) {
+                const float hv = h[t * 128 + c];
+#pragma unroll
+                for (int q = 0; q < kHrRows; ++q)
+                    acc[q] = __builtin_fmaf(hv, src[(size_t)q * cols + t], acc[q]);
+            }
+        }
+    } else {
+        for (int t = 0; t < 128; ++t) {
+            const float hv = h[t * 128 + c];
+            for (int q = 0; q < nr; ++q)
+                acc[q] = __builtin_fmaf(hv, src[(size_t)q * cols + t], acc[q]);
+        }
+    }
+    float* dst = out + (size_t)r0 * cols + 128 * b + c;
+#pragma unroll
+    for (int q = 0; q < kHrRows; ++q)
+        if (q < nr) dst[(size_t)q * cols] = acc[q];
 }
 
 template <int K>
@@ -1523,39 +1646,24 @@ __global__ __launch_bounds__(kFwdThreads) void ldlq_chain_kernel(
                 // wave-uniform step count: full buffers if the wave holds
                 // one, else block i's own buffer; shorter lanes feed zeros,
                 // whose products leave the accumulator unchanged
-                const int nqw = bw < qi ? 4 * pbuf : (bw == qi ? 4 * (cur - i - 1) : 0);
+                const int nqw = __builtin_amdgcn_readfirstlane(
+                    bw < qi ? 4 * pbuf : (bw == qi ? 4 * (cur - i - 1) : 0));
                 v16f acc;
 #pragma unroll
                 for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
                 if (nqw > 0) {
-                    typedef __attribute__((address_space(1))) const v4f gv4_t;
-                    const float* la = Lq + (size_t)i * 16 * k + (size_t)(mlo >> 2) * 64 + 4 * rc;
-                    const float* eb = Eq + (size_t)j * 16 * k + (size_t)(mlo >> 2) * 64 + 4 * rc;
-                    const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
-                    v4f pa[kFbPrefetch], pe[kFbPrefetch];
-                    // every load is issued at a valid address (clamped), its
-                    // value zeroed past the lane's buffer
-                    auto ld = [&](int sl, int mq) {
-                        const int mc = mq < nq ? mq : (nq > 0 ? nq - 1 : 0);
-                        const v4f a = *(gv4_t*)(la + mc * 64), e = *(gv4_t*)(eb + mc * 64);
-                        pa[sl] = mq < nq ? a : z;
-                        pe[sl] = mq < nq ? e : z;
-                    };
-#pragma unroll
-                    for (int p = 0; p < kFbPrefetch; ++p) ld(p, p);
-                    for (int mq0 = 0; mq0 < nqw; mq0 += kFbPrefetch) {
-#pragma unroll
-                        for (int u = 0; u < kFbPrefetch; ++u) {
-                            const v4f a = pa[u], e = pe[u];
-                            ld(u, mq0 + u + kFbPrefetch);
-                            if (mq0 + u < nqw) {
-                                acc = __builtin_amdgcn_mfma_f32_16x16x1f32(a.x, e.x, acc, 0, 0, 0);
-                                acc = __builtin_amdgcn_mfma_f32_16x16x1f32(a.y, e.y, acc, 0, 0, 0);
-                                acc = __builtin_amdgcn_mfma_f32_16x16x1f32(a.z, e.z, acc, 0, 0, 0);
-                                acc = __builtin_amdgcn_mfma_f32_16x16x1f32(a.w, e.w, acc, 0, 0, 0);
-                            }
-                        }
-                    }
+                    // L's column block i and E's column block j (wave-uniform
+                    // bases) at the lane's offset: the first m-quad of its
+                    // buffer, column rc
+                    const gbyte_t* const lb = uniform_gptr((uint8_t*)(Lq + (size_t)i * 16 * k));
+                    const gbyte_t* const eb = uniform_gptr((uint8_t*)(Eq + (size_t)j * 16 * k));
+                    const uint32_t off0 = 4u * ((uint32_t)(mlo >> 2) * 64u + 4u * (uint32_t)rc);
+                    // every lane of the wave runs nqw m-quads unless the wave
+                    // holds block i's own buffer or a buffer past it
+                    if (bw + 3 < qi)
+                        acc = fb_chain<false>(lb, eb, off0, nq, nqw);
+                    else
+                        acc = fb_chain<true>(lb, eb, off0, nq, nqw);
                 }
                 // accumulator register v = 4 blk' + t of lane (q, c): block
                 // blk', row 4q + t, column c
@@ -1564,8 +1672,21 @@ __global__ __launch_bounds__(kFwdThreads) void ldlq_chain_kernel(
                     P[(4 * wv + (v >> 2)) * 256 + (4 * blk + (v & 3)) * 16 + rc] = acc[v];
                 __syncthreads();
                 if (tid < 256) {
+                    // the round's partials in buffer order, read eight at a
+                    // time so that one LDS latency covers eight adds
                     const int nr = (nbuf - b0) < 64 ? (nbuf - b0) : 64;
-                    for (int sl = 0; sl < nr; ++sl) {
+                    int sl = 0;
+                    for (; sl + 8 <= nr; sl += 8) {
+                        float v[8];
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) v[u] = P[(sl + u) * 256 + tid];
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) {
+                            if (b0 + sl + u < qi) prod = prod + v[u];
+                            else gin = v[u];
+                        }
+                    }
+                    for (; sl < nr; ++sl) {
                         const float v = P[sl * 256 + tid];
                         if (b0 + sl < qi) prod = prod + v;
                         else gin = v;
@@ -1913,6 +2034,17 @@ hipError_t launch_had_left(const float* ht, const float* in, float* out, int row
     if (rows % 128 || rows / 128 > 65535) return hipErrorInvalidValue;
     hipLaunchKernelGGL(had_left_kernel, dim3((cols + 63) / 64, rows / 128, 2), dim3(256), 0,
                        stream, ht, in, out, cols);
+    return hipGetLastError();
+}
+
+hipError_t launch_had_right(const float* h, const float* in, float* out, int rows, int cols,
+                            hipStream_t stream) {
+    if (rows <= 0 || cols <= 0) return hipSuccess;
+    if (cols % 128) return hipErrorInvalidValue;
+    const int ry = (rows + 4 * kHrRows - 1) / (4 * kHrRows);
+    if (ry > 65535) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(had_right_kernel, dim3(cols / 64, ry), dim3(256), 0, stream, h, in, out,
+                       rows, cols);
     return hipGetLastError();
 }
 

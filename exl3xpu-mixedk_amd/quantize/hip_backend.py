@@ -64,6 +64,7 @@ def lib():
         L.xtq_trellis_unpack_dev.argtypes = [vp, i32, i32, vp, vp]
         L.xtq_vit_get_lut.argtypes = [cp, vp]
         L.xtq_had128_left_dev.argtypes = [vp, vp, vp, i32, i32, vp]
+        L.xtq_had128_right_dev.argtypes = [vp, vp, vp, i32, i32, vp]
         L.xtq_vit_scratch_per_seq.argtypes = [i32]
         L.xtq_vit_scratch_per_seq.restype = i64
         L.xtq_vit_chunk_seqs.argtypes = [i32, i32, ctypes.POINTER(ctypes.c_int)]
@@ -80,7 +81,8 @@ def lib():
                    "xtq_vit_tailbite_dev_async", "xtq_vit_tailbite_dev_noalloc", "xtq_vit_status_dev", "xtq_vit_viterbi_dev",
                    "xtq_ldlq_chain_dev", "xtq_ldlq_chain_multi_dev",
                    "xtq_trellis_decode_dev", "xtq_trellis_pack_dev",
-                   "xtq_trellis_unpack_dev", "xtq_vit_get_lut", "xtq_had128_left_dev"):
+                   "xtq_trellis_unpack_dev", "xtq_vit_get_lut", "xtq_had128_left_dev",
+                   "xtq_had128_right_dev"):
             getattr(L, fn).restype = i32
         _LIB = L
     return _LIB
@@ -272,6 +274,27 @@ def had128_left(w: torch.Tensor, h: torch.Tensor) -> torch.Tensor:
         rc = lib().xtq_had128_left_dev(ht.data_ptr(), w.data_ptr(), out.data_ptr(), w.shape[0],
                                        w.shape[1], _stream(w.device))
     _check("xtq_had128_left_dev", rc)
+    return out
+
+
+def had128_right(w: torch.Tensor, h: torch.Tensor) -> torch.Tensor:
+    """w @ blockdiag(h) for w [k, n] fp32 (device, n a multiple of 128) and
+    any 128x128 h on the same device: each output one fused multiply-add
+    chain in ascending order, as torch's CPU sgemm evaluates the reference's
+    matmul (xtq_had128_right_dev)."""
+    w = _dev_tensor(w, torch.float32, "w")
+    h = _dev_tensor(h, torch.float32, "h")
+    if w.dim() != 2 or w.shape[1] % 128 or h.shape != (128, 128) or h.device != w.device:
+        raise ValueError(f"had128_right needs w [k, 128m] and h [128, 128] on one device, got "
+                         f"{tuple(w.shape)}, {tuple(h.shape)}")
+    out = torch.empty_like(w)
+    if w.numel() == 0:
+        return out
+    with torch.cuda.device(w.device):
+        hc = h.contiguous()
+        rc = lib().xtq_had128_right_dev(hc.data_ptr(), w.data_ptr(), out.data_ptr(), w.shape[0],
+                                        w.shape[1], _stream(w.device))
+    _check("xtq_had128_right_dev", rc)
     return out
 
 

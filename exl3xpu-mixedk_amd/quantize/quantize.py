@@ -145,13 +145,12 @@ def had_left(w: torch.Tensor, h: torch.Tensor) -> torch.Tensor:
 
 def had_right(w: torch.Tensor, h: torch.Tensor) -> torch.Tensor:
     """Block-128 Hadamard applied on the last (n) dim of w [k, n]
-    (quantize.py:141-145); on the GPU the left transform of the transpose,
-    w @ h = (h^T @ w^T)^T (for the symmetric Hadamard the same products in
-    the same order as the CPU matmul)."""
+    (quantize.py:141-145).  GPU tensors go through the library's kernel,
+    which accumulates every output in the order torch's CPU matmul does."""
     k, n = w.shape
     assert n % 128 == 0
     if w.is_cuda and w.dtype == torch.float32:
-        return had_left(w.t().contiguous(), h.t()).t().contiguous()
+        return _hb.had128_right(w.contiguous(), h.to(w.device, torch.float32))
     return torch.matmul(w.view(k, n // 128, 128), h).view(k, n)
 
 

@@ -264,11 +264,24 @@ XTQ_API int xtq_trellis_unpack_dev(const int16_t* d_trellis, int nt, int K, int3
  * is symmetric, so it is passed as it is.  Each output is one fp32 fused
  * multiply-add chain over the 128 products in ascending order, as torch's
  * CPU sgemm evaluates the reference's matmul, so results equal the
- * reference's CPU results bit for bit.  had_right is this entry on the
- * transpose.  Stream-ordered.
+ * reference's CPU results bit for bit.  Stream-ordered.
  */
 XTQ_API int xtq_had128_left_dev(const float* d_ht, const float* d_in, float* d_out, int rows,
                                 int cols, void* stream);
+
+/*
+ * Device-pointer block-128 transform on the last dimension: the HIP
+ * counterpart of had_right (quantize.py:141-145).  d_h holds the [128][128]
+ * multipliers, d_h[t][c] the weight of input column t in output column c,
+ * so d_out = d_in @ blockdiag(d_h) for [rows][cols] fp32 row-major buffers
+ * (cols a multiple of 128, rows up to 2,097,120, d_out not d_in).  Each
+ * output is one fp32 fused multiply-add chain over the 128 products in
+ * ascending order, as torch's CPU sgemm evaluates the reference's matmul
+ * (the products and order of xtq_had128_left_dev on the transpose), so
+ * results equal the reference's CPU results bit for bit.  Stream-ordered.
+ */
+XTQ_API int xtq_had128_right_dev(const float* d_h, const float* d_in, float* d_out, int rows,
+                                 int cols, void* stream);
 
 /*
  * Copies the fp32 decode table of `code` (65536 entries) into host memory

@@ -247,6 +247,21 @@ def test_hadamard_kernel_matches_cpu(xq, k, n):
         torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("rows", [1, 7, 37, 1000])
+def test_had_right_ragged_rows(xq, rows):
+    """had_right on the GPU for row counts that leave a partial wave (the
+    kernel takes 8 rows per wave): each output row depends on its own input
+    row only, so the rows of the CPU product of a 1024-row matrix are the
+    reference (a shape whose CPU sgemm is one FMA chain per output)."""
+    g = torch.Generator().manual_seed(rows)
+    w = torch.randn(1024, 384, generator=g)
+    h = xq.hadamard128(None, torch.float32)
+    print(f"case had_right rows={rows}", flush=True)
+    want = xq.had_right(w, h)[:rows]
+    got = xq.had_right(w[:rows].contiguous().cuda(), h.cuda()).cpu()
+    assert torch.equal(got, want)
+
+
 def test_quantize_harness_golden(xq, cpu8):
     e = load_golden("e2e_128.npz")
     Wt = torch.from_numpy(e["prep_Wt"])
