@@ -104,6 +104,18 @@ def test_status_codes_without_device(lib):
     assert chm(fake, None, 64, 64, 9, i2(32, 32), i2(4, 7), *args, tp2, None, None) == 6
     assert chm(fake, None, 64, 64, 2, i2(32, 32), i2(4, 7), *args, tp1, None, None) == 12
     assert chm(fake, None, 64, 64, 2, None, i2(4, 7), *args, tp2, None, None) == 12
+    # block-128 Hadamard entries: pointers and shapes are checked before any launch
+    fake2 = ctypes.c_void_p(48)
+    hl, hr = lib.xtq_had128_left_dev, lib.xtq_had128_right_dev
+    assert hl(None, fake, fake2, 128, 64, None) == 12
+    assert hl(fake, fake, fake, 128, 64, None) == 12          # in place
+    assert hl(fake, fake, fake2, 100, 64, None) == 6          # rows not a multiple of 128
+    assert hl(fake, fake, fake2, 128, 0, None) == 6
+    assert hr(fake, None, fake2, 64, 128, None) == 12
+    assert hr(fake, fake, fake, 64, 128, None) == 12          # in place
+    assert hr(fake, fake, fake2, 64, 100, None) == 6          # cols not a multiple of 128
+    assert hr(fake, fake, fake2, 0, 128, None) == 6
+    assert hr(fake, fake, fake2, 2_097_121, 128, None) == 6   # one row past the documented maximum
     assert lib.xtq_vit_strerror(11) == b"NaN target"
     assert lib.xtq_vit_strerror(13) == b"synchronous entry given a stream under graph capture"
     assert lib.xtq_vit_strerror(99) == b"unknown status"
