@@ -730,27 +730,48 @@ def main():
     # and of the min-only mix of pass 1's first `pivot` steps (no backpointer
     # kept: v_min3_f32 tree, 3.5 instructions per candidate), weighted by the
     # sequence-steps of each kind per tile
+    # (the min-only mix issues 3.5 instructions for the 4 algorithmic ops of a
+    # candidate, so its ceiling in algorithmic ops is 4/3.5 of its issue rate)
     mix = "fp32-code candidate mix"
-    ceil_key = max(probes[f"{mix}, dependency order"], probes[f"{mix}, grouped by opcode"])
-    ceil_min = probes["deferred-argmin mix (3.5 instructions per candidate), grouped by opcode"]
+    mix_min = "deferred-argmin mix (3.5 instructions per candidate), grouped by opcode"
     n1 = PIVOT + MARGIN if 0 < MARGIN and PIVOT + MARGIN < 256 else 256
     s_min = min(PIVOT, n1 - 1)
     s_all = n1 + 256
-    ceil = s_all / ((s_all - s_min) / ceil_key + s_min / ceil_min)
+
+    def weighted(key_rate, min_rate):
+        ops_min = min_rate * OPS_PER_STATE_STEP / 3.5
+        return key_rate, ops_min, s_all / ((s_all - s_min) / key_rate + s_min / ops_min)
+
+    ceil_key, ceil_min, ceil = weighted(
+        max(probes[f"{mix}, dependency order"], probes[f"{mix}, grouped by opcode"]),
+        probes[mix_min])
     roofline["mix_ceiling"] = {"value": round(ceil, 3), "unit": "TFLOP/s",
                                "mix": f"{mix} on {s_all - s_min} of {s_all} sequence-steps "
                                       f"per tile, min-only mix on {s_min}",
                                "key_steps_ceiling": round(ceil_key, 3),
                                "min_only_steps_ceiling": round(ceil_min, 3),
                                "frac": round(achieved / ceil, 4),
+                               "occupancy": "two 1024-thread workgroups per CU (8 waves "
+                                            "per SIMD)",
                                "probe_tlane_instr_per_s": {k: round(v, 2)
                                                            for k, v in probes.items()}}
+    # the same mixes at the forward kernel's own occupancy: its 64 fp32
+    # codebook registers per lane leave room for one 1024-thread workgroup
+    # per CU (4 waves per SIMD)
+    k1, m1, c1 = weighted(probes[f"{mix}, grouped by opcode, one workgroup per CU"],
+                          probes[f"{mix_min}, one workgroup per CU"])
+    roofline["mix_ceiling_at_occupancy"] = {
+        "value": round(c1, 3), "unit": "TFLOP/s", "key_steps_ceiling": round(k1, 3),
+        "min_only_steps_ceiling": round(m1, 3), "frac": round(achieved / c1, 4),
+        "occupancy": "one 1024-thread workgroup per CU (4 waves per SIMD), the forward "
+                     "kernel's: 64 codebook VGPRs per lane leave room for no second one"}
     roofline["ceiling_note"] = (
         "0.5 of the published 157.3 TFLOP/s is the 78.65 T that one-op-per-lane "
         "instructions reach: the exact path issues four such instructions per "
         "candidate state (no FMA, no packed fp32), so 0.5 is out of reach by "
         "construction; the bar reported against is the measured issue ceiling of "
-        "the kernel's own instruction mix (mix_ceiling)")
+        "the kernel's own instruction mix (mix_ceiling), also measured at the "
+        "kernel's occupancy (mix_ceiling_at_occupancy)")
     tfile = os.path.join(ROOT, "profiles", "fwd_kernel_K4_traffic.json")
     if os.path.exists(tfile):
         with open(tfile) as f:

@@ -26,8 +26,15 @@ constexpr int kIters = 500;
 constexpr int kChains = 16;
 constexpr int kThreads = 1024;
 
-template <int OP>
+// ONE: the kernel also holds 96 KiB of LDS, so that one workgroup (16
+// waves, 4 per SIMD) runs per CU at a time -- the forward DP's occupancy,
+// whose 64 codebook VGPRs per lane leave room for no second workgroup --
+// instead of two (8 waves per SIMD).
+constexpr int kOneWgLds = 96 * 1024 / 4;
+
+template <int OP, bool ONE = false>
 __global__ __launch_bounds__(kThreads) void probe_kernel(float* __restrict__ out, float b) {
+    __shared__ float pad[ONE ? kOneWgLds : 1];
     float x[kChains];
     double d[kChains];
     uint32_t h[kChains];
@@ -134,15 +141,22 @@ __global__ __launch_bounds__(kThreads) void probe_kernel(float* __restrict__ out
     float s = 0.0f;
 #pragma unroll
     for (int c = 0; c < kChains; ++c) s += x[c] + (float)d[c];
+    if constexpr (ONE) {
+        // touch the LDS block so that it is allocated
+        pad[threadIdx.x] = s;
+        __syncthreads();
+        s += pad[kThreads - 1 - threadIdx.x];
+    }
     out[(size_t)blockIdx.x * kThreads + threadIdx.x] = s;
 }
 
 // VALU instructions per chain per iteration of each probe.
-constexpr double kOpsPerChain[11] = {1, 1, 1, 1, 1, 4, 4, 4, 4, 1, 3.5};
+constexpr double kOpsPerChain[13] = {1, 1, 1, 1, 1, 4, 4, 4, 4, 1, 3.5, 4, 3.5};
 
-template <int OP>
+template <int OP, bool ONE = false>
 hipError_t launch(int nwg, float* out, hipStream_t s) {
-    hipLaunchKernelGGL(probe_kernel<OP>, dim3(nwg), dim3(kThreads), 0, s, out, 1.0000001f);
+    hipLaunchKernelGGL((probe_kernel<OP, ONE>), dim3(nwg), dim3(kThreads), 0, s, out,
+                       1.0000001f);
     return hipGetLastError();
 }
 
@@ -158,7 +172,9 @@ hipError_t launch_any(int which, int nwg, float* out, hipStream_t s) {
         case 7: return launch<7>(nwg, out, s);
         case 8: return launch<8>(nwg, out, s);
         case 9: return launch<9>(nwg, out, s);
-        default: return launch<10>(nwg, out, s);
+        case 10: return launch<10>(nwg, out, s);
+        case 11: return launch<8, true>(nwg, out, s);
+        default: return launch<10, true>(nwg, out, s);
     }
 }
 
@@ -169,13 +185,15 @@ hipError_t launch_any(int which, int nwg, float* out, hipStream_t s) {
 // dependency order / grouped by opcode, 7/8 the mix with an fp32 codebook in
 // dependency order / grouped by opcode, 9 v_min3_f32, 10 the deferred-argmin
 // mix: add, mul, add per candidate and a v_min3_f32 tree over 8 -- 3.5
-// instructions per candidate) on every CU of the current device
-// and returns its VALU lane-instructions per second.  Status: 0 ok, 1 no
-// device, 2 allocation failed, 4 HIP error, 8 unknown probe, 12 null output.
+// instructions per candidate; 11 and 12 the mixes of 8 and 10 at one
+// workgroup per CU, the forward DP's occupancy) on every CU of the current
+// device and returns its VALU lane-instructions per second.  Status: 0 ok,
+// 1 no device, 2 allocation failed, 4 HIP error, 8 unknown probe, 12 null
+// output.
 extern "C" __attribute__((visibility("default"))) int xtq_valu_probe(int which,
                                                                      double* lane_ops_per_s) {
     if (!lane_ops_per_s) return 12;
-    if (which < 0 || which > 10) return 8;
+    if (which < 0 || which > 12) return 8;
     int dev = 0, ncu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||

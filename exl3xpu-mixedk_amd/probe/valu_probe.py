@@ -15,7 +15,10 @@ PROBES = ("v_mul_f32", "v_add_f32", "v_fma_f32", "v_fma_mix_f32", "v_min_f64",
           "candidate mix, dependency order", "candidate mix, grouped by opcode",
           "fp32-code candidate mix, dependency order",
           "fp32-code candidate mix, grouped by opcode", "v_min3_f32",
-          "deferred-argmin mix (3.5 instructions per candidate), grouped by opcode")
+          "deferred-argmin mix (3.5 instructions per candidate), grouped by opcode",
+          "fp32-code candidate mix, grouped by opcode, one workgroup per CU",
+          "deferred-argmin mix (3.5 instructions per candidate), grouped by opcode, "
+          "one workgroup per CU")
 
 _LIB = None
 

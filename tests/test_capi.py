@@ -157,7 +157,7 @@ def test_probe_library_is_separate(lib):
     import valu_probe
     pl = valu_probe.lib()
     v = ctypes.c_double()
-    assert pl.xtq_valu_probe(11, ctypes.byref(v)) == 8
+    assert pl.xtq_valu_probe(13, ctypes.byref(v)) == 8
     assert pl.xtq_valu_probe(-1, ctypes.byref(v)) == 8
     assert pl.xtq_valu_probe(0, None) == 12
 

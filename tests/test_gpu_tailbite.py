@@ -334,10 +334,17 @@ def test_valu_probe_rates():
     import valu_probe
     ncu = torch.cuda.get_device_properties(0).multi_processor_count
     base = ncu * 64 * 2.4e9
+    rates = {}
     for i, name in enumerate(valu_probe.PROBES):
         r = valu_probe.rate(i)
+        rates[name] = r
         print(f"probe {name}: {r / 1e12:.2f} T/s", flush=True)
         assert 0.5 * base < r < 2.5 * base, (name, r)
+    # a mix at one workgroup per CU (4 waves per SIMD) issues no faster than
+    # with two (8 waves per SIMD) beside it
+    for mix in ("fp32-code candidate mix, grouped by opcode",
+                "deferred-argmin mix (3.5 instructions per candidate), grouped by opcode"):
+        assert rates[mix + ", one workgroup per CU"] < 1.05 * rates[mix], mix
 
 
 def test_async_encode_and_status(hb, oracle_mod, mul1_lut):
