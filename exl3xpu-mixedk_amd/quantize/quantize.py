@@ -31,6 +31,7 @@ from __future__ import annotations
 import math
 import os
 import sys
+import threading
 import time
 
 import numpy as np
@@ -200,20 +201,55 @@ _STAGE_MIN = 1 << 20
 _STAGE: list = []
 
 
-def _to_host(t: torch.Tensor) -> torch.Tensor:
+class _HostBuffers:
+    """Host tensors of the given (shape, dtype) specs, allocated and every
+    4 KiB page of them touched in a background thread.  The first-touch page
+    faults of a fresh tensor otherwise set the pace of a large copy into it:
+    c5's 356 MB fp32 W_hat took 11-20 ms from the staging buffers into fresh
+    memory and 4.4 ms into touched memory, against 6.3 ms for the DMA.
+    Started before the long device phase (its synchronous library calls
+    release the interpreter lock), so the faults are taken while the host
+    waits for the GPU."""
+
+    def __init__(self, specs):
+        specs = [(tuple(int(x) for x in shape), dtype) for shape, dtype in specs]
+        self._bufs = [None] * len(specs)
+        self._thread = threading.Thread(target=self._fill, args=(specs,), daemon=True)
+        self._thread.start()
+
+    def _fill(self, specs):
+        for i, (shape, dtype) in enumerate(specs):
+            t = torch.empty(shape, dtype=dtype)
+            if t.numel():
+                t.view(-1).view(torch.uint8)[::4096].zero_()
+            self._bufs[i] = t
+
+    def take(self, i: int):
+        """Buffer i (None if the thread could not make it); each is handed
+        out once."""
+        self._thread.join()
+        t, self._bufs[i] = self._bufs[i], None
+        return t
+
+
+def _to_host(t: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """t.cpu() for device tensors of 1 MiB or more through two pinned staging
     buffers (allocated once per process): chunk i+1's device-to-host DMA runs
-    while chunk i is copied into the (pageable) result.  Measured on the
-    MI355X host: 126 MB in 3.9 ms, against 31 ms on the runtime's pageable
-    path (~4 GB/s from 64 MB up); 21 MB in 0.5 ms against 1.2 ms.  Smaller
-    tensors and host tensors take t.cpu()."""
+    while chunk i is copied into the (pageable) result -- `out` when given
+    (a contiguous host tensor of t's shape and dtype, e.g. from
+    _HostBuffers), else a new tensor.  Measured on the MI355X host: 126 MB
+    in 3.9 ms, against 31 ms on the runtime's pageable path (~4 GB/s from
+    64 MB up); 21 MB in 0.5 ms against 1.2 ms.  Smaller tensors and host
+    tensors take t.cpu()."""
     if not t.is_cuda or t.numel() * t.element_size() < _STAGE_MIN:
         return t.cpu()
     if not _STAGE:
         _STAGE.extend(torch.empty(_STAGE_BYTES, dtype=torch.uint8, pin_memory=True)
                       for _ in range(2))
     src = t.contiguous().view(-1).view(torch.uint8)
-    out = torch.empty(t.shape, dtype=t.dtype)
+    if (out is None or out.is_cuda or out.shape != t.shape or out.dtype != t.dtype
+            or not out.is_contiguous()):
+        out = torch.empty(t.shape, dtype=t.dtype)
     dst = out.view(-1).view(torch.uint8)
     n, C = src.numel(), _STAGE_BYTES
     offs = list(range(0, n, C))
@@ -646,6 +682,13 @@ def quantize_linear_group(Ws, H_x: torch.Tensor | None, code: str = "exl3_mul1",
         if progress is not None:
             progress("hinv", time.time() - t0)
 
+    # the results' host tensors (W_hat, trellis per member), paged in during
+    # the sweep (after the factorisation, whose host side it would share the
+    # cores with)
+    outbufs = _HostBuffers([spec for W, Km in zip(Ws, Ks) for spec in (
+        (W.shape, torch.float32),
+        ((k_in // 16, W.shape[0] // 16, 16 * Km), torch.int16))]) if dev.type != "cpu" else None
+
     # runs of consecutive members with the same K: (first column, columns, K)
     runs = []
     for mb, Km in zip(members, Ks):
@@ -703,7 +746,7 @@ def quantize_linear_group(Ws, H_x: torch.Tensor | None, code: str = "exl3_mul1",
         assert torch.equal(hw, hatWq[:, c0:c0 + nc].to(hw.device)), "decode != encoder output"
         hatW_parts.append(hw)
     out, off = [], 0
-    for mb, Km in zip(members, Ks):
+    for mi, (mb, Km) in enumerate(zip(members, Ks)):
         n = mb["n"]
         ri = max(i for i, r in enumerate(runs) if r[0] <= off)
         c0 = off - runs[ri][0]
@@ -718,8 +761,8 @@ def quantize_linear_group(Ws, H_x: torch.Tensor | None, code: str = "exl3_mul1",
         else:
             W_hat = from_inner(hatW_d * Wscale, suh, svh, h).t().contiguous()
         out.append({
-            "W_hat": _to_host(W_hat),
-            "trellis": _to_host(tr),
+            "W_hat": _to_host(W_hat, outbufs.take(2 * mi) if outbufs else None),
+            "trellis": _to_host(tr, outbufs.take(2 * mi + 1) if outbufs else None),
             "suh": suh.cpu(), "svh": svh.cpu(),
             "Wscale": float(Wscale), "lut_rms": float(lut_rms),
             "code": code, "K": Km, "L": L, "V": V, "use_ldlq": use_ldlq,

@@ -277,6 +277,14 @@ def test_to_host_staging(xq):
         h = xq._to_host(t.view(-1, 1) if n % 2 else t.view(2, -1))
         assert h.device.type == "cpu" and not h.is_pinned()
         assert torch.equal(h.view(-1), t.cpu())
+    # into a given buffer (paged in beforehand) when it matches, else a new tensor
+    t = torch.randn(3 * C // 4 + 5, device="cuda")
+    bufs = xq._HostBuffers([(t.shape, torch.float32), (t.shape, torch.float64),
+                            ((t.numel() - 1,), torch.float32)])
+    for i, same in ((0, True), (1, False), (2, False)):
+        b = bufs.take(i)
+        h = xq._to_host(t, b)
+        assert (h.data_ptr() == b.data_ptr()) == same and torch.equal(h, t.cpu())
 
 
 @pytest.mark.parametrize("Ks,device", [((5, 7, 7), "cuda"), ((4, 6, 4), "cuda"),

@@ -31,6 +31,18 @@ def test_get_lut_small_L(xq, oracle_mod):
                                   oracle_mod.code_lut("exl3_mul1", 8))
 
 
+def test_host_buffers(xq):
+    """The background-allocated result buffers have the requested shapes
+    and dtypes, are contiguous host tensors, and are handed out once."""
+    specs = [((40, 1024), torch.float32), ((3, 2, 48), torch.int16), ((0,), torch.float32)]
+    bufs = xq._HostBuffers(specs)
+    for i, (shape, dt) in enumerate(specs):
+        t = bufs.take(i)
+        assert t.shape == shape and t.dtype == dt and t.is_contiguous()
+        assert t.device.type == "cpu"
+        assert bufs.take(i) is None
+
+
 def test_perm_golden(xq):
     np.testing.assert_array_equal(xq.tensor_core_perm().numpy(),
                                   load_golden("lut_mul1.npz")["perm"])
