@@ -199,6 +199,16 @@ def _check_viterbi_args(L: int, V: int, dtype, emit_mode: str):
 _STAGE_BYTES = 32 << 20
 _STAGE_MIN = 1 << 20
 _STAGE: list = []
+# the staging buffers serve one copy at a time (calls from several threads
+# take turns)
+_STAGE_LOCK = threading.Lock()
+
+
+def _stage_buffers() -> list:
+    if not _STAGE:
+        _STAGE.extend(torch.empty(_STAGE_BYTES, dtype=torch.uint8, pin_memory=True)
+                      for _ in range(2))
+    return _STAGE
 
 
 class _HostBuffers:
@@ -243,9 +253,6 @@ def _to_host(t: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     tensors take t.cpu()."""
     if not t.is_cuda or t.numel() * t.element_size() < _STAGE_MIN:
         return t.cpu()
-    if not _STAGE:
-        _STAGE.extend(torch.empty(_STAGE_BYTES, dtype=torch.uint8, pin_memory=True)
-                      for _ in range(2))
     src = t.contiguous().view(-1).view(torch.uint8)
     if (out is None or out.is_cuda or out.shape != t.shape or out.dtype != t.dtype
             or not out.is_contiguous()):
@@ -253,23 +260,56 @@ def _to_host(t: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     dst = out.view(-1).view(torch.uint8)
     n, C = src.numel(), _STAGE_BYTES
     offs = list(range(0, n, C))
-    stream = torch.cuda.current_stream(t.device)
-    ev = [torch.cuda.Event(), torch.cuda.Event()]
+    with _STAGE_LOCK, torch.cuda.device(t.device):
+        stage = _stage_buffers()
+        stream = torch.cuda.current_stream(t.device)
+        ev = [torch.cuda.Event(), torch.cuda.Event()]
 
-    def issue(i):
-        o = offs[i]
-        m = min(C, n - o)
-        _STAGE[i & 1][:m].copy_(src[o:o + m], non_blocking=True)
-        ev[i & 1].record(stream)
+        def issue(i):
+            o = offs[i]
+            m = min(C, n - o)
+            stage[i & 1][:m].copy_(src[o:o + m], non_blocking=True)
+            ev[i & 1].record(stream)
 
-    with torch.cuda.device(t.device):
         issue(0)
         for i, o in enumerate(offs):
             if i + 1 < len(offs):
                 issue(i + 1)      # its buffer's previous chunk was copied out at i - 1
             ev[i & 1].synchronize()
             m = min(C, n - o)
-            dst[o:o + m].copy_(_STAGE[i & 1][:m])
+            dst[o:o + m].copy_(stage[i & 1][:m])
+    return out
+
+
+def _to_device(t: torch.Tensor, dev: torch.device) -> torch.Tensor:
+    """t.to(dev) for host tensors of 1 MiB or more through the two pinned
+    staging buffers: chunk i is copied into buffer i & 1 while chunk i-1's
+    host-to-device DMA runs; the call returns with every DMA complete (the
+    buffers are free for the next copy).  Measured on the MI355X host:
+    1.21 GB in 22 ms against 40 ms through the runtime's pageable path,
+    67 MB in 1.6 ms against 2.3 ms.  Device tensors, CPU targets and smaller
+    tensors take t.to(dev)."""
+    dev = torch.device(dev)
+    if (t.is_cuda or dev.type != "cuda"
+            or t.numel() * t.element_size() < _STAGE_MIN):
+        return t.to(dev)
+    src = t.contiguous().view(-1).view(torch.uint8)
+    out = torch.empty(t.shape, dtype=t.dtype, device=dev)
+    dst = out.view(-1).view(torch.uint8)
+    n, C = src.numel(), _STAGE_BYTES
+    with _STAGE_LOCK, torch.cuda.device(dev):
+        stage = _stage_buffers()
+        stream = torch.cuda.current_stream(dev)
+        ev = [torch.cuda.Event(), torch.cuda.Event()]
+        for i, o in enumerate(range(0, n, C)):
+            m = min(C, n - o)
+            if i >= 2:
+                ev[i & 1].synchronize()         # chunk i-2's DMA out of this buffer
+            stage[i & 1][:m].copy_(src[o:o + m])
+            dst[o:o + m].copy_(stage[i & 1][:m], non_blocking=True)
+            ev[i & 1].record(stream)
+        for e in ev:
+            e.synchronize()
     return out
 
 
@@ -643,7 +683,7 @@ def quantize_linear_group(Ws, H_x: torch.Tensor | None, code: str = "exl3_mul1",
         m_out = W.shape[0]
         suh = suh0
         svh = sign_vec(m_out, su_seed + 1, dev).half()
-        W32 = W.float().to(dev).t().contiguous()          # [k, n]
+        W32 = _to_device(W, dev).float().t().contiguous()  # [k, n]
         mb = {"n": m_out}
         if channel_scales:
             su, sv = suh.float(), svh.float()
@@ -671,13 +711,13 @@ def quantize_linear_group(Ws, H_x: torch.Tensor | None, code: str = "exl3_mul1",
     Lfac = None
     if use_ldlq and H_x is not None:
         t0 = time.time()
-        G = rotate_hessian(H_x.float().to(dev), suh0, h)
+        G = rotate_hessian(_to_device(H_x.float(), dev), suh0, h)
         dead = G.diagonal() == 0
         if dead.any():
             G[dead, dead] = 1.0
         G.diagonal().add_((percdamp * red(G.diagonal()).mean()).to(dev))
         # the reference factors on the CPU on every device (quantize.py:816)
-        Lfac = _factor_hessian(red(G)).to(dev, Wq.dtype)
+        Lfac = _to_device(_factor_hessian(red(G)).to(Wq.dtype), dev)
         del G
         if progress is not None:
             progress("hinv", time.time() - t0)
@@ -867,7 +907,7 @@ def prepare_incoherence(W: torch.Tensor, H_x: torch.Tensor | None = None,
             else su_sign.to(dev).half())
     sv_s = (sign_vec(m_out, (su_seed + 1) if sv_seed is None else sv_seed, dev).half()
             if sv_sign is None else sv_sign.to(dev).half())
-    W32 = W.float().to(dev).t().contiguous()
+    W32 = _to_device(W, dev).float().t().contiguous()
     if channel_scales:
         su, sv = su_s.float(), sv_s.float()
         sv_mag = W32.square().mean(dim=0).sqrt()
@@ -888,7 +928,8 @@ def prepare_incoherence(W: torch.Tensor, H_x: torch.Tensor | None = None,
         su_mag = torch.ones(k_in, device=dev)
         sv_mag = torch.ones(m_out, device=dev)
         zero_out = torch.zeros(m_out, dtype=torch.bool, device=dev)
-    G = rotate_hessian(H_x.float().to(dev), su_s, h).cpu() if H_x is not None else None
+    G = _to_host(rotate_hessian(_to_device(H_x.float(), dev), su_s, h)) \
+        if H_x is not None else None
     return {"Wt": W_i.t().contiguous().cpu(), "G": G,
             "suh": suh.cpu(), "svh": svh.cpu(),
             "su_mag": su_mag.cpu(), "sv_mag": sv_mag.cpu(),

@@ -264,8 +264,9 @@ def test_quantize_linear_group_matches_separate(xq, cs, ldlq):
 
 
 def test_to_host_staging(xq):
-    """The staged device-to-host copy equals .cpu() for sizes around its
-    threshold and around and across the staging chunks, for several dtypes."""
+    """The staged device-to-host and host-to-device copies equal .cpu() and
+    .to("cuda") for sizes around their threshold and around and across the
+    staging chunks, for several dtypes."""
     C, M = xq._STAGE_BYTES, xq._STAGE_MIN
     for nbytes, dt in ((M - 4, torch.float32), (M, torch.float32), (M + 2, torch.int16),
                        (C - 8, torch.float64), (C, torch.float32), (C + 6, torch.int16),
@@ -277,6 +278,9 @@ def test_to_host_staging(xq):
         h = xq._to_host(t.view(-1, 1) if n % 2 else t.view(2, -1))
         assert h.device.type == "cpu" and not h.is_pinned()
         assert torch.equal(h.view(-1), t.cpu())
+        # and back through the staged host-to-device copy
+        d = xq._to_device(h, torch.device("cuda"))
+        assert d.is_cuda and d.shape == h.shape and torch.equal(d.view(-1), t)
     # into a given buffer (paged in beforehand) when it matches, else a new tensor
     t = torch.randn(3 * C // 4 + 5, device="cuda")
     bufs = xq._HostBuffers([(t.shape, torch.float32), (t.shape, torch.float64),
@@ -528,3 +532,18 @@ def test_chain_factor_over_2g_elements(hb, oracle_mod, mul1_lut):
         want = oracle_mod.tailbite(xt[i].cpu().numpy(), mul1_lut, 4, 16, pivot=128, margin=0)
         np.testing.assert_array_equal(st[i].cpu().numpy(), want)
     del L
+
+
+def test_weight_widening_on_device_matches_host():
+    """quantize_linear moves a host weight to the GPU in its own dtype and
+    widens it to fp32 there: for every fp16 and bf16 bit pattern (subnormals
+    included) the device conversion gives the host conversion's fp32 bits
+    (NaNs: NaN either way)."""
+    u = torch.arange(65536, dtype=torch.int32).to(torch.int16)
+    for dt in (torch.float16, torch.bfloat16):
+        x = u.view(dt)
+        host = x.float()
+        dev = x.cuda().float().cpu()
+        nan = torch.isnan(host)
+        assert torch.equal(torch.isnan(dev), nan)
+        assert torch.equal(dev[~nan].view(torch.int32), host[~nan].view(torch.int32)), dt
