@@ -313,6 +313,16 @@ def _to_device(t: torch.Tensor, dev: torch.device) -> torch.Tensor:
     return out
 
 
+def _weight_fp32(W: torch.Tensor, dev: torch.device) -> torch.Tensor:
+    """W as fp32 on dev.  fp16 and bf16 host weights cross in their own dtype
+    (half the bytes) and are widened on the device, which gives the host
+    conversion's bits for every bit pattern; other dtypes are converted
+    where they are, as before the copy."""
+    if W.dtype in (torch.float16, torch.bfloat16):
+        return _to_device(W, dev).float()
+    return _to_device(W.float(), dev)
+
+
 def _on_gpu(X: torch.Tensor) -> torch.Tensor:
     if X.is_cuda:
         return X
@@ -683,7 +693,7 @@ def quantize_linear_group(Ws, H_x: torch.Tensor | None, code: str = "exl3_mul1",
         m_out = W.shape[0]
         suh = suh0
         svh = sign_vec(m_out, su_seed + 1, dev).half()
-        W32 = _to_device(W, dev).float().t().contiguous()  # [k, n]
+        W32 = _weight_fp32(W, dev).t().contiguous()       # [k, n]
         mb = {"n": m_out}
         if channel_scales:
             su, sv = suh.float(), svh.float()
@@ -907,7 +917,7 @@ def prepare_incoherence(W: torch.Tensor, H_x: torch.Tensor | None = None,
             else su_sign.to(dev).half())
     sv_s = (sign_vec(m_out, (su_seed + 1) if sv_seed is None else sv_seed, dev).half()
             if sv_sign is None else sv_sign.to(dev).half())
-    W32 = _to_device(W, dev).float().t().contiguous()
+    W32 = _weight_fp32(W, dev).t().contiguous()
     if channel_scales:
         su, sv = su_s.float(), sv_s.float()
         sv_mag = W32.square().mean(dim=0).sqrt()
