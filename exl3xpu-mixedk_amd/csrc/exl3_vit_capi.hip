@@ -119,6 +119,10 @@ struct DevCtx {
     float* hx = nullptr;       // staging for the host-pointer entries
     int32_t* hs = nullptr;
     size_t host_cap = 0;
+    // pinned host staging of the host-pointer entries' states (grow-only,
+    // host memory, not counted in `owned`)
+    int32_t* hpin = nullptr;
+    size_t hpin_cap = 0;       // elements
     size_t owned = 0;          // device bytes held
     // Recorded on the stream of the last call that used the scratch above;
     // the next call waits for it on its own stream, and growing the scratch
@@ -887,9 +891,33 @@ int run_host(const float* X, int nseq, int K, Code code, int margin, int pivot,
                        hipSuccess)
             rc = 4;
         if (!rc) rc = run_tailbite(cx, cx.hx, nseq, K, code, margin, pivot, cx.hs, nullptr, 0);
-        if (!rc && hipMemcpy(out, cx.hs, (size_t)nseq * xtq::kSteps * 4, hipMemcpyDeviceToHost) !=
-                       hipSuccess)
+        // The states come back through pinned staging (a DMA at full PCIe
+        // rate, then one host copy): the runtime's pageable path copies
+        // device-to-host at a few GB/s.  Without the staging (allocation
+        // failed) they take that path.
+        const size_t nel = (size_t)nseq * xtq::kSteps;
+        if (!rc && nel > cx.hpin_cap) {
+            if (cx.hpin) (void)hipHostFree(cx.hpin);
+            cx.hpin = nullptr;
+            cx.hpin_cap = 0;
+            if (hipHostMalloc((void**)&cx.hpin, nel * sizeof(int32_t), hipHostMallocDefault) ==
+                hipSuccess) {
+                cx.hpin_cap = nel;
+            } else {
+                cx.hpin = nullptr;
+                (void)hipGetLastError();   // not left for a later launch check to report
+            }
+        }
+        if (!rc && cx.hpin) {
+            if (hipMemcpy(cx.hpin, cx.hs, nel * sizeof(int32_t), hipMemcpyDeviceToHost) !=
+                hipSuccess)
+                rc = 4;
+            else
+                memcpy(out, cx.hpin, nel * sizeof(int32_t));
+        } else if (!rc && hipMemcpy(out, cx.hs, nel * sizeof(int32_t), hipMemcpyDeviceToHost) !=
+                              hipSuccess) {
             rc = 4;
+        }
     }
     if (dev != prev) (void)hipSetDevice(prev);
     return rc;
