@@ -11,7 +11,9 @@
  *   - every entry point returns an int status, 0 on success; nothing throws
  *     across the ABI; diagnostics go to stderr;
  *   - the caller owns all input and output buffers; the library owns a
- *     per-device, grow-only device scratch it never frees;
+ *     per-device, grow-only device scratch it never frees (and, for the
+ *     host-pointer entries, a grow-only pinned host buffer of the last
+ *     call's states, nseq * 1 KiB);
  *   - one caller at a time per process (calls are serialised internally by a
  *     mutex, but concurrent callers gain nothing);
  *   - X is [nseq][256] fp32, C-contiguous, one sequence per tile in the
