@@ -722,12 +722,19 @@ def quantize_linear_group(Ws, H_x: torch.Tensor | None, code: str = "exl3_mul1",
     if use_ldlq and H_x is not None:
         t0 = time.time()
         G = rotate_hessian(_to_device(H_x.float(), dev), suh0, h)
+        if host:
+            # the damping and the factorisation on a host copy of the whole
+            # G, as the reference computes them (quantize.py:809-816): its
+            # damping mean runs over the strided diagonal view of the [k, k]
+            # matrix, and torch's CPU mean of a contiguous copy of that
+            # diagonal can round differently
+            G = _to_host(G)
         dead = G.diagonal() == 0
         if dead.any():
             G[dead, dead] = 1.0
-        G.diagonal().add_((percdamp * red(G.diagonal()).mean()).to(dev))
+        G.diagonal().add_(percdamp * G.diagonal().mean())
         # the reference factors on the CPU on every device (quantize.py:816)
-        Lfac = _to_device(_factor_hessian(red(G)).to(Wq.dtype), dev)
+        Lfac = _to_device(_factor_hessian(G).to(Wq.dtype), dev)
         del G
         if progress is not None:
             progress("hinv", time.time() - t0)

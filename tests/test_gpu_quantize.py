@@ -192,6 +192,34 @@ def test_reference_arithmetic_equals_cpu_pipeline(xq, cpu8, cs):
     assert rg["Wscale"] == rc["Wscale"]
 
 
+@pytest.mark.parametrize("n,k,K,code,cs,buf,rho,seed", [
+    (384, 768, 7, "exl3_3inst", False, 32, 0.4673059694552129, 1198),
+    (1024, 768, 7, "exl3_mcg", True, 16, 0.770254471100988, 1005),
+])
+def test_reference_arithmetic_damping_mean_layout(xq, cpu8, n, k, K, code, cs, buf, rho, seed):
+    """Weights whose damped Gram's diagonal mean rounds differently over the
+    strided diagonal view of the [k, k] matrix (the reference's
+    G.diagonal().mean(), quantize.py:813) than over a contiguous copy of the
+    diagonal: reference_arithmetic on the GPU must take the mean over the
+    same view, or the factor, and with it the feedback of every later tile,
+    differs from device="cpu" (a random sweep found one such case in 100)."""
+    import workloads as wl
+    g = torch.Generator().manual_seed(seed)
+    W = (0.02 * torch.randn(n, k, generator=g)).half().float()
+    H = wl.ar1_gram(k, k // 2, rho, seed)
+    suh = xq.sign_vec(k, 20261011, "cpu").half()
+    G = xq.rotate_hessian(H, suh, xq.hadamard128("cpu", torch.float32))
+    assert G.diagonal().mean() != G.diagonal().contiguous().mean()    # the case this pins
+    args = dict(code=code, K=K, margin=0, channel_scales=cs, buf_cols=buf)
+    print(f"case damping-mean layout W {n}x{k} K={K} {code} cs={cs} buf={buf}", flush=True)
+    rc = xq.quantize_linear(W, H, device="cpu", **args)
+    rg = xq.quantize_linear(W.cuda(), H.cuda(), device="cuda", reference_arithmetic=True, **args)
+    bad = int((rg["trellis"] != rc["trellis"]).any(dim=-1).sum())
+    assert bad == 0, f"{bad} of {(k // 16) * (n // 16)} tiles differ"
+    for key in ("W_hat", "suh", "svh"):
+        assert torch.equal(rg[key], rc[key]), key
+
+
 def test_reference_arithmetic_mixed_k_group(xq, cpu8):
     """quantize_linear_group of q/k/v-like members at K = [5, 7, 7] with
     channel scales on the GPU under reference_arithmetic (concurrent chain
