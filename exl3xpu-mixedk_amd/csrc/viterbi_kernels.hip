@@ -1336,7 +1336,8 @@ __global__ __launch_bounds__(64) void pack_kernel(const int32_t* __restrict__ st
 // blocks read in the matrix-core operand layout described below), runs
 // both tail-biting passes with in-workgroup tracebacks,
 // writes the states, the packed trellis, What and E for the tile, and
-// publishes the tile with a release store of the launch's epoch.  A task
+// publishes the tile by storing the launch's epoch into its flag once E's
+// write-through stores have completed.  A task
 // only waits for a task taken before it, whose workgroup is running, so the
 // waits always end; columns advance independently, so the GPU is not left
 // half idle at the end of every block the way block-synchronous launches of
@@ -1735,19 +1736,31 @@ __global__ __launch_bounds__(kFwdThreads) void ldlq_chain_kernel(
             const float w = lut[s];
             hatW[g] = w;
             const int m = 16 * i + (pe >> 4);                 // E in the quad layout
-            Eq[(size_t)j * 16 * k + (size_t)(m >> 2) * 64 + 4 * (pe & 15) + (m & 3)] = W[g] - w;
+            // E is all that other workgroups read of the tile (their
+            // feedback, on any XCD): an agent-scope store (sc1) writes it
+            // through this XCD's L2, visible agent-wide once it completes
+            __hip_atomic_store(&Eq[(size_t)j * 16 * k + (size_t)(m >> 2) * 64 + 4 * (pe & 15) +
+                                   (m & 3)],
+                               W[g] - w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (states) states[tile * kSteps + tid] = s;
         } else if (tid < kSteps + 8 * K) {
             const int wd = tid - kSteps;
             store_word(trellis + ((size_t)i * tnl + jl) * 16 * K + 2 * wd, pack_word<K>(st, wd));
         }
-        // every wave's stores complete (explicitly: the barrier's
-        // workgroup-scope release does not wait for them) before thread 0's
-        // agent-scope release publishes them all with one L2 write-back
+        // Every wave's stores complete before the barrier (explicitly: the
+        // barrier's workgroup-scope release does not wait for them), so E's
+        // write-through stores are visible agent-wide before thread 0 stores
+        // the flag, which therefore cannot overtake them; the waiter's
+        // acquire fence then invalidates its L2 before it reads E.  A release
+        // store here would add an L2 write-back of every dirty line of the
+        // XCD (buffer_wbl2: the other workgroups' backpointer rows among
+        // them), which no waiter needs -- the rest of the tile (W_hat,
+        // states, trellis) is read only after the launch.  c5 K=4: 950
+        // against 958 ms per sweep, results identical.
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if (tid == 0) {
-            __hip_atomic_store(flags + tile, epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(flags + tile, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             task = atomicAdd(counter, 1);
         }
     }
