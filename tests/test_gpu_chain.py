@@ -178,6 +178,26 @@ def test_chain_one_long_column(xq, hb, oracle_mod, mul1_lut):
     _check_tiles(oracle_mod, mul1_lut, 3, 128, 0, st, tr, xt)
 
 
+@pytest.mark.parametrize("k,n,K", [(1024, 16, 4), (2048, 48, 6)])
+def test_chain_publish_between_launches(xq, hb, oracle_mod, mul1_lut, k, n, K):
+    """Narrow weights (1 and 3 column chains for 256 workgroups): almost
+    every task waits for its predecessor's flag and reads that tile's E at
+    once.  Four launches in a row on different weights reuse the library's
+    E scratch, so a tile read before its E was visible would return the
+    previous launch's error and miss the targets bound; every tile's
+    targets and states are checked in every launch."""
+    L = _lfac(xq, k, 11)
+    perm = xq.tensor_core_perm()
+    for rep in range(4):
+        g = torch.Generator().manual_seed(300 + 10 * K + rep)
+        W = torch.randn(k, n, generator=g) * (1.0 + rep)
+        print(f"case chain publish K={K} {k}x{n} launch {rep}", flush=True)
+        hatW, st, tr, xt = (t.cpu() for t in hb.ldlq_chain(W.cuda(), L.cuda(), K, 128, 0,
+                                                            targets=True))
+        _check_targets(W, L, hatW, xt, perm)
+        _check_tiles(oracle_mod, mul1_lut, K, 128, 0, st, tr, xt)
+
+
 def test_chain_many_tasks_per_workgroup(xq, hb, oracle_mod, mul1_lut):
     """2048 tiles: several tasks per persistent workgroup; targets of every
     tile checked, states of the first and last block rows at both edges."""
