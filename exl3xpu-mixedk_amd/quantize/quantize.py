@@ -57,9 +57,23 @@ def _f16(bits) -> np.ndarray:
     return np.asarray(bits).astype(np.uint16).view(np.float16)
 
 
+_CODE_TABLES: dict = {}
+
+
 def _code_table(name: str, L: int) -> np.ndarray:
     """fp32 decode table of a named V=1 code over all 2^L states
-    (the codes of quantize.py:56-87)."""
+    (the codes of quantize.py:56-87), computed once per (code, L) and kept
+    read-only (get_lut hands out copies)."""
+    key = (name, int(L))
+    t = _CODE_TABLES.get(key)
+    if t is None:
+        t = _code_table_compute(name, int(L))
+        t.setflags(write=False)
+        _CODE_TABLES[key] = t
+    return t
+
+
+def _code_table_compute(name: str, L: int) -> np.ndarray:
     s = np.arange(1 << L, dtype=np.uint64)
     if name == "exl3_mul1":
         h = (s * 0x83DCD12D) & 0xFFFFFFFF
@@ -177,10 +191,19 @@ def rotate_hessian(H_x: torch.Tensor, suh: torch.Tensor, h: torch.Tensor) -> tor
     return had_right(had_right(a.view(k, k), h).t().contiguous(), h)
 
 
+_SIGNS: dict = {}
+
+
 def sign_vec(n: int, seed: int, device=None) -> torch.Tensor:
-    """Deterministic Rademacher vector from torch's CPU generator."""
-    g = torch.Generator().manual_seed(seed)
-    return torch.where(torch.rand(n, generator=g) < 0.5, -1.0, 1.0).to(device)
+    """Deterministic Rademacher vector from torch's CPU generator (drawn once
+    per (n, seed); every call returns a tensor of its own)."""
+    key = (int(n), int(seed))
+    v = _SIGNS.get(key)
+    if v is None:
+        g = torch.Generator().manual_seed(seed)
+        v = _SIGNS[key] = torch.where(torch.rand(n, generator=g) < 0.5, -1.0, 1.0)
+    dev = torch.device(device) if device is not None else torch.device("cpu")
+    return v.clone() if dev.type == "cpu" else v.to(dev)
 
 
 # ------------------------------------------------------------------ Viterbi

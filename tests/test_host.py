@@ -55,6 +55,20 @@ def test_sign_vec_golden(xq):
             np.testing.assert_array_equal(xq.sign_vec(n, s).numpy(), g[f"sign_{n}_{s}"])
 
 
+def test_cached_tables_hand_out_own_tensors(xq):
+    """get_lut and sign_vec compute their values once per key: writing into
+    a returned tensor must not change what later calls return."""
+    g = load_golden("sign_vec.npz")
+    v = xq.sign_vec(256, 7)
+    v.fill_(3.0)
+    np.testing.assert_array_equal(xq.sign_vec(256, 7).numpy(), g["sign_256_7"])
+    lut = xq.get_lut("exl3_mul1", 16)
+    want = lut.clone()
+    lut.zero_()
+    assert torch.equal(xq.get_lut("exl3_mul1", 16), want)
+    assert not xq._code_table("exl3_mul1", 16).flags.writeable
+
+
 def test_hadamard_closed_form(xq):
     h = xq.hadamard128(None, torch.float64)
     assert torch.allclose(h @ h, torch.eye(128, dtype=torch.float64), atol=1e-14)
