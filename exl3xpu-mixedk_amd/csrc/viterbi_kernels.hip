@@ -261,6 +261,15 @@ constexpr int kChunkWMin = kChunkW<K, T>;
 template <int K>
 constexpr int kPrioTop = K == 3 ? 1 : 2;
 
+// Whether a K=4 key step stores the lane's first two group minima as soon as
+// they are final, so that the LDS writes overlap the two remaining groups'
+// trees (the other two leave at the end of the step): batched K=4 at four
+// sequences per workgroup 431.1k / 431.7k -> 433.9k / 434.4k tiles/s (same
+// box, alternating runs, states identical); the column chain (one sequence)
+// 947-948 -> 949 ms, so not there.
+template <int K, int T>
+constexpr bool kEarlyPair = (K == 4 && T >= 2);
+
 // Whether a sequence-step recomputes the lane's offsets instead of keeping
 // them live (see fwd_run): measured faster for one sequence per workgroup
 // at K = 2, 3 (the column chain: 5120x5120 sweep K=2 -3 %, K=3 -6 %; K=2
@@ -476,6 +485,11 @@ __device__ __forceinline__ void fwd_run(
                         v[NCH] = run[c];
                         run[c] = fmin_tree<NCH + 1>(v);
                     }
+                    if constexpr (KEYS && kEarlyPair<K, T>) {
+                        if (qc == NCHUNK - 1 && c == 1 && i + 1 < nsteps)
+                            lds_store_cost2<0>(lds_addr(bbuf[tt][(i + 1) & 1] + bslot<K>(jb)),
+                                               run[0], run[1]);
+                    }
                     if constexpr (K == 2) {
                         // K=2's 16 costs per lane leave in 16-byte quads as
                         // soon as each quad of groups is done, overlapping
@@ -505,6 +519,8 @@ __device__ __forceinline__ void fwd_run(
                 float* bnext = bbuf[tt][(i + 1) & 1] + bslot<K>(jb);
                 if constexpr (K == 2) {
                     // stored per quad of groups above
+                } else if constexpr (KEYS && kEarlyPair<K, T>) {
+                    lds_store_cost2<2>(lds_addr(bnext), run[2], run[3]);  // 0, 1 above
                 } else if constexpr (KEYS && (G::C == 2 || G::C == 4)) {
                     lds_store_costs<G::C>(lds_addr(bnext), run);
                 } else if constexpr (G::C == 2) {
