@@ -246,8 +246,12 @@ constexpr int kChunkWMin = kChunkW<K, T>;
 // passes fixed points of its step's work, so that waves ahead yield the
 // SIMD to those behind and all arrive together.  Points, in units of
 // (sequence, chunk, group) of the step: K >= 5 drop to 1 at 5/8 and to 0 at
-// 7/8, K = 4 to 1 at half and to 0 at three quarters (at 1/4 and 5/8 for a
-// single sequence, the column chain: -1 % there), K = 3 to 0 at three
+// 7/8, K = 4 to 1 at half and to 0 at seven eighths with four sequences
+// per workgroup (three quarters before the early pair stores of kEarlyPair;
+// with them 7/8 measured +0.8 %: 435.4k -> 438.9k tiles/s, 13/16, 27/32 and
+// 29/32 in between, 15/16 -0.9 %, no second drop -4 %), at three quarters
+// with two, at 1/4 and 5/8 for a single sequence (the column chain: -1 %
+// there), K = 3 to 0 at three
 // quarters, K = 2 (one chunk of 4-candidate groups) to 1 right after the
 // step's target is read and to 0 after a quarter of its groups (the column
 // chain -3 % against dropping to 0 at the target read).  Measured against no priorities (same box,
@@ -422,8 +426,10 @@ __device__ __forceinline__ void fwd_run(
                         const int pos = (tt * NCHUNK + qc) * G::C + c;
                         // drop points, as fractions of the step's units
                         constexpr int D1 = K >= 5 ? U * 5 / 8 : T == 1 ? U / 4 : U / 2;
-                        constexpr int D0 = K >= 5 ? U * 7 / 8 : K == 4 && T == 1 ? U * 5 / 8
-                                                                                  : U * 3 / 4;
+                        constexpr int D0 = K >= 5                ? U * 7 / 8
+                                           : K == 4 && T == 1 ? U * 5 / 8
+                                           : K == 4 && T == 4 ? U * 7 / 8
+                                                              : U * 3 / 4;
                         if constexpr (K >= 4) {
                             if (pos == D1) __builtin_amdgcn_s_setprio(1);
                         }
