@@ -250,8 +250,12 @@ constexpr int kChunkWMin = kChunkW<K, T>;
 // per workgroup (three quarters before the early pair stores of kEarlyPair;
 // with them 7/8 measured +0.8 %: 435.4k -> 438.9k tiles/s, 13/16, 27/32 and
 // 29/32 in between, 15/16 -0.9 %, no second drop -4 %), at three quarters
-// with two, at 1/4 and 5/8 for a single sequence (the column chain: -1 %
-// there), K = 3 to 0 at three
+// with two, and for a single sequence (the column chain) to 1 as soon as the
+// step's target and first minima are read (unit 0) and to 0 at 7/8 (c5 K=4
+// sweep 946-948 -> 917 ms, c3 271.6-271.8 -> 263 ms, against the 1/4 and
+// 5/8 used before; 1 and 7 units, 2 and 6 or 7, 0 and 6 in between; never
+// dropping to 0 +3 %; a first drop at 0 is 3-4 % slower for four sequences
+// and for the K = 5, 6 chains), K = 3 to 0 at three
 // quarters, K = 2 (one chunk of 4-candidate groups) to 1 right after the
 // step's target is read and to 0 after a quarter of its groups (the column
 // chain -3 % against dropping to 0 at the target read).  Measured against no priorities (same box,
@@ -425,9 +429,12 @@ __device__ __forceinline__ void fwd_run(
                         constexpr int U = T * NCHUNK * G::C;  // units of a step
                         const int pos = (tt * NCHUNK + qc) * G::C + c;
                         // drop points, as fractions of the step's units
-                        constexpr int D1 = K >= 5 ? U * 5 / 8 : T == 1 ? U / 4 : U / 2;
+                        constexpr int D1 = K >= 5                ? U * 5 / 8
+                                           : K == 4 && T == 1 ? 0
+                                           : T == 1           ? U / 4
+                                                              : U / 2;
                         constexpr int D0 = K >= 5                ? U * 7 / 8
-                                           : K == 4 && T == 1 ? U * 5 / 8
+                                           : K == 4 && T == 1 ? U * 7 / 8
                                            : K == 4 && T == 4 ? U * 7 / 8
                                                               : U * 3 / 4;
                         if constexpr (K >= 4) {
