@@ -257,15 +257,17 @@ constexpr int kChunkWMin = kChunkW<K, T>;
 // dropping to 0 +3 %; a first drop at 0 is 3-4 % slower for four sequences
 // and for the K = 5, 6 chains), K = 3 to 0 at three
 // quarters, K = 2 (one chunk of 4-candidate groups) to 1 right after the
-// step's target is read and to 0 after a quarter of its groups (the column
-// chain -3 % against dropping to 0 at the target read).  Measured against no priorities (same box,
+// step's target is read and to 0 after three quarters of its groups
+// (batched 343k -> 360k tiles/s, the 5120x5120 column chain 308 -> 294 ms,
+// against the quarter used before; 1/8 .. 15/16 of the groups and no drop
+// to 0 scanned, every other point slower; the drop to 1 moved into the
+// groups 2-4 % slower).  Measured against no priorities (same box,
 // alternating runs): batched K = 2..7 256k/339k/360k/364k/358k/352k ->
 // 311k/371k/391k/392k/391k/390k tiles/s with K >= 5 on the K = 4 points,
 // which K >= 5's own add 1 % to (and 2.5 % to their column chain, where
 // K = 4 loses 2 % with them); the 5120x5120 column chain at K = 2..7
-// -10/-3/-3/-11/-9/-9 %.  Slower: later drops for K = 2 (294k at three
-// quarters), other points or a third level for K = 3, a fourth level for
-// K >= 4.
+// -10/-3/-3/-11/-9/-9 %.  Slower: other points or a third level for K = 3,
+// a fourth level for K >= 4.
 template <int K>
 constexpr int kPrioTop = K == 3 ? 1 : 2;
 
@@ -423,7 +425,7 @@ __device__ __forceinline__ void fwd_run(
                 for (int c = 0; c < G::C; ++c) {
                     const int blk = c / G::CB;
                     if constexpr (K == 2) {
-                        if (c == G::C / 4) __builtin_amdgcn_s_setprio(0);
+                        if (c == G::C * 3 / 4) __builtin_amdgcn_s_setprio(0);
                     }
                     if constexpr (K >= 3) {
                         constexpr int U = T * NCHUNK * G::C;  // units of a step
