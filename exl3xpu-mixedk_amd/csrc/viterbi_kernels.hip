@@ -246,7 +246,8 @@ constexpr int kChunkWMin = kChunkW<K, T>;
 // passes fixed points of its step's work, so that waves ahead yield the
 // SIMD to those behind and all arrive together.  Points, in units of
 // (sequence, chunk, group) of the step: K >= 5 drop to 1 at 5/8 and to 0 at
-// 7/8, K = 4 to 1 at half and to 0 at seven eighths with four sequences
+// 7/8 (rescanned last: 15/16 for the second drop, 1/2 or 3/4 for the first,
+// and 0 for the first in the column chain, all slower), K = 4 to 1 at half and to 0 at seven eighths with four sequences
 // per workgroup (three quarters before the early pair stores of kEarlyPair;
 // with them 7/8 measured +0.8 %: 435.4k -> 438.9k tiles/s, 13/16, 27/32 and
 // 29/32 in between, 15/16 -0.9 %, no second drop -4 %), at three quarters
@@ -255,8 +256,10 @@ constexpr int kChunkWMin = kChunkW<K, T>;
 // sweep 946-948 -> 917 ms, c3 271.6-271.8 -> 263 ms, against the 1/4 and
 // 5/8 used before; 1 and 7 units, 2 and 6 or 7, 0 and 6 in between; never
 // dropping to 0 +3 %; a first drop at 0 is 3-4 % slower for four sequences
-// and for the K = 5, 6 chains), K = 3 to 0 at three
-// quarters, K = 2 (one chunk of 4-candidate groups) to 1 right after the
+// and for the K = 5, 6 chains), K = 3 to 0 at 5/8 (batched 389.9k ->
+// 394.9k tiles/s, the 5120x5120 column chain 294.1 -> 287.3 ms, against the
+// three quarters used before; 3/8, 1/2 and 7/8 slower), K = 2 (one chunk
+// of 4-candidate groups) to 1 right after the
 // step's target is read and to 0 after three quarters of its groups
 // (batched 343k -> 360k tiles/s, the 5120x5120 column chain 308 -> 294 ms,
 // against the quarter used before; 1/8 .. 15/16 of the groups and no drop
@@ -438,6 +441,7 @@ __device__ __forceinline__ void fwd_run(
                         constexpr int D0 = K >= 5                ? U * 7 / 8
                                            : K == 4 && T == 1 ? U * 7 / 8
                                            : K == 4 && T == 4 ? U * 7 / 8
+                                           : K == 3           ? U * 5 / 8
                                                               : U * 3 / 4;
                         if constexpr (K >= 4) {
                             if (pos == D1) __builtin_amdgcn_s_setprio(1);
