@@ -256,9 +256,11 @@ constexpr int kChunkWMin = kChunkW<K, T>;
 // sweep 946-948 -> 917 ms, c3 271.6-271.8 -> 263 ms, against the 1/4 and
 // 5/8 used before; 1 and 7 units, 2 and 6 or 7, 0 and 6 in between; never
 // dropping to 0 +3 %; a first drop at 0 is 3-4 % slower for four sequences
-// and for the K = 5, 6 chains), K = 3 to 0 at 5/8 (batched 389.9k ->
-// 394.9k tiles/s, the 5120x5120 column chain 294.1 -> 287.3 ms, against the
-// three quarters used before; 3/8, 1/2 and 7/8 slower), K = 2 (one chunk
+// and for the K = 5, 6 chains), K = 3 to 1 at the step's first group and
+// to 0 at 5/8 (one level, 1 -> 0 at three quarters, before: batched 389.9k
+// -> 394.9k tiles/s and the 5120x5120 column chain 294.1 -> 287.3 ms with
+// the drop at 5/8, then 396k -> 405k with the second level; 3/8, 1/2, 3/4
+// and 7/8 slower), K = 2 (one chunk
 // of 4-candidate groups) to 1 right after the
 // step's target is read and to 0 after three quarters of its groups
 // (batched 343k -> 360k tiles/s, the 5120x5120 column chain 308 -> 294 ms,
@@ -269,10 +271,9 @@ constexpr int kChunkWMin = kChunkW<K, T>;
 // 311k/371k/391k/392k/391k/390k tiles/s with K >= 5 on the K = 4 points,
 // which K >= 5's own add 1 % to (and 2.5 % to their column chain, where
 // K = 4 loses 2 % with them); the 5120x5120 column chain at K = 2..7
-// -10/-3/-3/-11/-9/-9 %.  Slower: other points or a third level for K = 3,
-// a fourth level for K >= 4.
+// -10/-3/-3/-11/-9/-9 %.  Slower: a fourth level for K >= 4.
 template <int K>
-constexpr int kPrioTop = K == 3 ? 1 : 2;
+constexpr int kPrioTop = 2;
 
 // Whether a K=4 key step stores the lane's first two group minima as soon as
 // they are final, so that the LDS writes overlap the two remaining groups'
@@ -436,6 +437,7 @@ __device__ __forceinline__ void fwd_run(
                         // drop points, as fractions of the step's units
                         constexpr int D1 = K >= 5                ? U * 5 / 8
                                            : K == 4 && T == 1 ? 0
+                                           : K == 3           ? 0
                                            : T == 1           ? U / 4
                                                               : U / 2;
                         constexpr int D0 = K >= 5                ? U * 7 / 8
@@ -443,9 +445,7 @@ __device__ __forceinline__ void fwd_run(
                                            : K == 4 && T == 4 ? U * 7 / 8
                                            : K == 3           ? U * 5 / 8
                                                               : U * 3 / 4;
-                        if constexpr (K >= 4) {
-                            if (pos == D1) __builtin_amdgcn_s_setprio(1);
-                        }
+                        if (pos == D1) __builtin_amdgcn_s_setprio(1);
                         if (pos == D0) __builtin_amdgcn_s_setprio(0);
                     }
                     // candidate costs fl(fl(fl(f - x)^2) + b)
